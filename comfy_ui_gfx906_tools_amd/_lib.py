@@ -1,0 +1,244 @@
+"""ctypes binding of libqlinear.so (C ABI in include/qlinear.h) for torch tensors.
+
+The reference binds its kernels through a pybind11 torch extension
+(nodes/ComfyUI-Gfx906Int4/csrc/binding.cpp:364-392). Here the boundary is a plain C ABI and
+this module is the thin Python side of it: it checks tensors, makes them contiguous (copies,
+like binding.cpp:89-90), allocates outputs and workspaces with torch's caching allocator,
+passes raw pointers plus the current HIP stream, and turns a non-zero status into
+RuntimeError carrying the library's message. There is no CPU fallback: a missing library or a
+CPU tensor is an error.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import threading
+
+import torch
+
+_PKG_DIR = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(_PKG_DIR, "libqlinear.so")
+
+# dtype codes of the C ABI (csrc/binding.cpp:45-50 of the reference, plus int32)
+QL_F32, QL_F16, QL_BF16, QL_I32 = 0, 1, 2, 3
+_DTYPE_CODE = {torch.float32: QL_F32, torch.float16: QL_F16, torch.bfloat16: QL_BF16, torch.int32: QL_I32}
+
+RULE_DIV = 0    # scale = amax / 7        (torch on CPU)
+RULE_RECIP = 1  # scale = amax * fl(1/7)  (torch on GPU; the reference kernel)
+
+_lib = None
+_lib_lock = threading.Lock()
+
+_c_size_t = ctypes.c_size_t
+_c_i64 = ctypes.c_int64
+_c_int = ctypes.c_int
+_c_vp = ctypes.c_void_p
+
+# name -> (restype, argtypes); must match include/qlinear.h
+SIGNATURES = {
+    "qlinear_last_error": (ctypes.c_char_p, []),
+    "qlinear_abi_version": (_c_int, []),
+    "qlinear_w4a16_workspace_bytes": (_c_size_t, [_c_i64, _c_i64, _c_i64, _c_int, _c_int]),
+    "qlinear_w4a16_gemm": (_c_int, [_c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,
+                                    _c_int, _c_vp, _c_size_t, _c_vp]),
+    "qlinear_w4a16_auto_splits": (_c_int, [_c_i64, _c_i64, _c_i64, _c_int]),
+    "qlinear_quantize_int4": (_c_int, [_c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
+    "qlinear_quantize_int8_per_token": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
+    "qlinear_w8a8_gemm": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp]),
+}
+
+
+def load_library(path: str = LIB_PATH):
+    """Load libqlinear.so once (thread-safe). Raises if it is missing: build it with
+    `python -m comfy_ui_gfx906_tools_amd.build`."""
+    global _lib
+    if _lib is not None:
+        return _lib
+    with _lib_lock:
+        if _lib is None:
+            if not os.path.exists(path):
+                raise RuntimeError(f"{path} is missing: build it with `python -m comfy_ui_gfx906_tools_amd.build` "
+                                   "(this engine has no CPU fallback)")
+            lib = ctypes.CDLL(path)
+            for name, (res, args) in SIGNATURES.items():
+                fn = getattr(lib, name)
+                fn.restype = res
+                fn.argtypes = args
+            _lib = lib
+    return _lib
+
+
+def _check(rc: int, what: str) -> None:
+    if rc != 0:
+        msg = load_library().qlinear_last_error().decode(errors="replace")
+        raise RuntimeError(f"{what} failed (status {rc}): {msg}")
+
+
+def _dev_tensor(t: torch.Tensor, name: str) -> torch.Tensor:
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a torch.Tensor, got {type(t).__name__}")
+    if t.device.type != "cuda":
+        raise RuntimeError(f"{name} must be on a GPU device, got {t.device} (no CPU fallback)")
+    t = t.contiguous()
+    if t.data_ptr() % 16:
+        t = t.clone()  # fresh caching-allocator block: 16-byte aligned
+    return t
+
+
+def _stream_ptr(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+class _Workspaces:
+    """Zero-initialised device workspaces, one per (device, stream): calls that share one must
+    be ordered, and work on one stream is. Grown on demand; the kernels leave the counter
+    area zero after every call."""
+
+    def __init__(self):
+        self._bufs: dict[tuple[int, int], torch.Tensor] = {}
+        self._lock = threading.Lock()
+
+    def get(self, device: torch.device, stream: int, nbytes: int) -> torch.Tensor:
+        key = (device.index, stream)
+        with self._lock:
+            buf = self._bufs.get(key)
+            if buf is None or buf.numel() < nbytes:
+                buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+                self._bufs[key] = buf
+            return buf
+
+
+_workspaces = _Workspaces()
+
+
+def w4a16_gemm(x: torch.Tensor, w_q4: torch.Tensor, w_scale: torch.Tensor, bias: torch.Tensor | None = None,
+               out_dtype: torch.dtype | None = None, splits: int = 0) -> torch.Tensor:
+    """y[M, N] = x[M, K] @ dequant(w_q4, w_scale)^T (+ bias) on the gfx950 W4A16 kernel.
+    x: bf16/fp16 [M, K]; w_q4: int8 [N, K/2]; w_scale: fp32 [N, K/32]; bias: out_dtype [N]."""
+    lib = load_library()
+    x = _dev_tensor(x, "x")
+    w_q4 = _dev_tensor(w_q4, "w_q4")
+    w_scale = _dev_tensor(w_scale, "w_scale")
+    if x.dtype not in (torch.bfloat16, torch.float16):
+        raise RuntimeError(f"x dtype {x.dtype} unsupported, expected bfloat16 or float16")
+    if w_q4.dtype not in (torch.int8, torch.uint8) or w_scale.dtype != torch.float32:
+        raise RuntimeError(f"w_q4 must be int8 and w_scale float32, got {w_q4.dtype} / {w_scale.dtype}")
+    if x.dim() != 2 or w_q4.dim() != 2:
+        raise RuntimeError(f"expected x [M, K] and w_q4 [N, K/2], got {tuple(x.shape)} / {tuple(w_q4.shape)}")
+    M, K = x.shape
+    N = w_q4.shape[0]
+    if w_q4.shape[1] * 2 != K or w_scale.numel() != N * (K // 32):
+        raise RuntimeError(f"expected w_q4 [{N}, {K // 2}] and w_scale [{N}, {K // 32}] for x [{M}, {K}], "
+                           f"got {tuple(w_q4.shape)} / {tuple(w_scale.shape)}")
+    if not (x.device == w_q4.device == w_scale.device):
+        raise RuntimeError(f"x, w_q4, w_scale must share a device, got {x.device} / {w_q4.device} / {w_scale.device}")
+    out_dtype = out_dtype or x.dtype
+    if out_dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        raise RuntimeError(f"out dtype {out_dtype} unsupported")
+    if bias is not None:
+        bias = _dev_tensor(bias, "bias")
+        if bias.dtype != out_dtype or bias.numel() != N:
+            raise RuntimeError(f"bias must be {out_dtype} [{N}], got {bias.dtype} {tuple(bias.shape)}")
+    y = torch.empty((M, N), dtype=out_dtype, device=x.device)
+    if M == 0:
+        return y
+    with torch.cuda.device(x.device):
+        stream = _stream_ptr(x.device)
+        nbytes = lib.qlinear_w4a16_workspace_bytes(M, N, K, splits, x.device.index)
+        ws = _workspaces.get(x.device, stream, nbytes) if nbytes else None
+        rc = lib.qlinear_w4a16_gemm(_DTYPE_CODE[x.dtype], _DTYPE_CODE[out_dtype], x.data_ptr(), w_q4.data_ptr(),
+                                    w_scale.data_ptr(), bias.data_ptr() if bias is not None else None, y.data_ptr(),
+                                    M, N, K, splits, ws.data_ptr() if ws is not None else None,
+                                    ws.numel() if ws is not None else 0, stream)
+    _check(rc, "w4a16_gemm")
+    return y
+
+
+def w4a16_auto_splits(M: int, N: int, K: int, device: torch.device | int | None = None) -> int:
+    """K pieces per tile that splits=0 resolves to for [M, K] x [N, K]^T (1 = unsplit)."""
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device("cuda", device) \
+        if isinstance(device, int) else device
+    rc = load_library().qlinear_w4a16_auto_splits(M, N, K, dev.index)
+    if rc < 0:
+        _check(-rc, "w4a16_auto_splits")
+    return rc
+
+
+def quantize_int4(x: torch.Tensor, rule: int = RULE_RECIP) -> tuple[torch.Tensor, torch.Tensor]:
+    """Block-32 int4 quantize + pack of a device tensor [..., K] -> (int8 [..., K/2], fp32 [..., K/32])."""
+    lib = load_library()
+    x = _dev_tensor(x, "x")
+    if x.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        raise RuntimeError(f"unsupported dtype {x.dtype}, expected float32/float16/bfloat16")
+    K = x.shape[-1]
+    if K % 32 != 0:
+        raise RuntimeError(f"last dim {K} not divisible by block 32")
+    rows = x.numel() // K if K else 0
+    packed = torch.empty((*x.shape[:-1], K // 2), dtype=torch.int8, device=x.device)
+    scale = torch.empty((*x.shape[:-1], K // 32), dtype=torch.float32, device=x.device)
+    if rows == 0:
+        return packed, scale
+    with torch.cuda.device(x.device):
+        rc = lib.qlinear_quantize_int4(_DTYPE_CODE[x.dtype], rule, x.data_ptr(), packed.data_ptr(), scale.data_ptr(),
+                                       rows, K, _stream_ptr(x.device))
+    _check(rc, "quantize_int4")
+    return packed, scale
+
+
+def quantize_int8_per_token(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-row int8 quantize: x [M, K] -> (int8 [M, K], fp32 [M])."""
+    lib = load_library()
+    x = _dev_tensor(x, "x")
+    if x.dtype not in (torch.float32, torch.float16, torch.bfloat16) or x.dim() != 2:
+        raise RuntimeError(f"x must be a float32/float16/bfloat16 [M, K] tensor, got {x.dtype} {tuple(x.shape)}")
+    M, K = x.shape
+    q = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    s = torch.empty((M,), dtype=torch.float32, device=x.device)
+    if M == 0:
+        return q, s
+    with torch.cuda.device(x.device):
+        rc = lib.qlinear_quantize_int8_per_token(_DTYPE_CODE[x.dtype], x.data_ptr(), q.data_ptr(), s.data_ptr(), M, K,
+                                                 _stream_ptr(x.device))
+    _check(rc, "quantize_int8_per_token")
+    return q, s
+
+
+def w8a8_gemm(xq: torch.Tensor, x_scale: torch.Tensor, wq: torch.Tensor, w_scale: torch.Tensor,
+              bias: torch.Tensor | None = None, out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """int8 x int8 -> int32 GEMM with per-token x per-channel rescale. out_dtype torch.int32
+    returns the raw accumulators."""
+    lib = load_library()
+    xq = _dev_tensor(xq, "xq")
+    wq = _dev_tensor(wq, "wq")
+    if xq.dtype != torch.int8 or wq.dtype != torch.int8 or xq.dim() != 2 or wq.dim() != 2:
+        raise RuntimeError(f"expected int8 xq [M, K] and wq [N, K], got {xq.dtype} {tuple(xq.shape)} / "
+                           f"{wq.dtype} {tuple(wq.shape)}")
+    M, K = xq.shape
+    N = wq.shape[0]
+    if wq.shape[1] != K:
+        raise RuntimeError(f"K mismatch: xq {tuple(xq.shape)} vs wq {tuple(wq.shape)}")
+    if out_dtype not in _DTYPE_CODE:
+        raise RuntimeError(f"out dtype {out_dtype} unsupported")
+    sx = sw = None
+    if out_dtype != torch.int32:
+        sx = _dev_tensor(x_scale, "x_scale")
+        sw = _dev_tensor(w_scale, "w_scale")
+        if sx.dtype != torch.float32 or sw.dtype != torch.float32 or sx.numel() != M or sw.numel() != N:
+            raise RuntimeError(f"scales must be float32 [{M}] / [{N}], got {sx.dtype} {tuple(sx.shape)} / "
+                               f"{sw.dtype} {tuple(sw.shape)}")
+        if bias is not None:
+            bias = _dev_tensor(bias, "bias")
+            if bias.dtype != out_dtype or bias.numel() != N:
+                raise RuntimeError(f"bias must be {out_dtype} [{N}], got {bias.dtype} {tuple(bias.shape)}")
+    else:
+        bias = None
+    y = torch.empty((M, N), dtype=out_dtype, device=xq.device)
+    if M == 0:
+        return y
+    with torch.cuda.device(xq.device):
+        rc = lib.qlinear_w8a8_gemm(_DTYPE_CODE[out_dtype], xq.data_ptr(), sx.data_ptr() if sx is not None else None,
+                                   wq.data_ptr(), sw.data_ptr() if sw is not None else None,
+                                   bias.data_ptr() if bias is not None else None, y.data_ptr(), M, N, K,
+                                   _stream_ptr(xq.device))
+    _check(rc, "w8a8_gemm")
+    return y

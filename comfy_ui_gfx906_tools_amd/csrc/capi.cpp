@@ -1,0 +1,276 @@
+// C ABI of libqlinear.so (include/qlinear.h): argument checks, launch planning, error text.
+// Counterpart of the reference's pybind11 layer (nodes/ComfyUI-Gfx906Int4/csrc/binding.cpp):
+// the same checks, expressed as status codes plus a per-thread message instead of
+// TORCH_CHECK exceptions; no tensor types cross this boundary.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <mutex>
+#include <string>
+
+#include "../../include/qlinear.h"
+#include "launch.hpp"
+
+using namespace qlinear;
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(buf, sizeof buf, fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int ok() {
+  g_last_error.clear();
+  return QL_OK;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+
+const char* dtype_name(int dt) {
+  switch (dt) {
+    case QL_F32: return "float32";
+    case QL_F16: return "float16";
+    case QL_BF16: return "bfloat16";
+    case QL_I32: return "int32";
+    default: return "unknown";
+  }
+}
+
+// CU count per device, queried once per device (callers may run on several threads).
+int device_cus(int device, int* cus) {
+  static std::mutex mu;
+  static int cache[256] = {0};
+  if (device < 0) {
+    if (hipGetDevice(&device) != hipSuccess) return fail(QL_ERR_DEVICE, "hipGetDevice failed");
+  }
+  if (device >= 256) return fail(QL_ERR_DEVICE, "device index %d out of range", device);
+  std::lock_guard<std::mutex> lock(mu);
+  if (cache[device] == 0) {
+    int v = 0;
+    const hipError_t e = hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, device);
+    if (e != hipSuccess || v <= 0)
+      return fail(QL_ERR_DEVICE, "hipDeviceGetAttribute(MultiprocessorCount, %d): %s", device, hipGetErrorString(e));
+    cache[device] = v;
+  }
+  *cus = cache[device];
+  return QL_OK;
+}
+
+// ---- W4A16 launch plan ---------------------------------------------------------------------
+// Tiles first go one per workgroup ("data-parallel"); when that leaves the last wave of a
+// 1-workgroup-per-CU grid badly filled, the tiles of that last wave are cut into ksplit K
+// pieces instead, chosen to minimise the modelled makespan (in tile-times).
+constexpr int kMaxCutTiles = QL_W4A16_COUNTER_BYTES / 4;  // one uint32 counter per cut tile
+
+struct W4A16Plan {
+  int cfg, BM, BN, tiles_m, tiles_n, stages, dp_tiles, ksplit, grid;
+  size_t counter_bytes, partial_bytes;
+};
+
+// Config 0 (256 x 256) is built but not selected: its cut-tile path still spills registers.
+int w4a16_cfg_for(int64_t M) {
+  if (M <= 16) return 3;
+  if (M <= 64) return 2;
+  return 1;
+}
+
+W4A16Plan plan_w4a16(int64_t M, int64_t N, int64_t K, int splits, int cus) {
+  W4A16Plan pl{};
+  pl.cfg = w4a16_cfg_for(M);
+  const W4A16Config& c = w4a16_config(pl.cfg);
+  pl.BM = c.BM;
+  pl.BN = c.BN;
+  pl.tiles_m = (int)((M + c.BM - 1) / c.BM);
+  pl.tiles_n = (int)((N + c.BN - 1) / c.BN);
+  pl.stages = (int)((K + 255) / 256);  // steps of two 128-K pipeline stages
+  const int tiles = pl.tiles_m * pl.tiles_n;
+  pl.dp_tiles = tiles;
+  pl.ksplit = 1;
+  if (splits >= 2 && tiles <= kMaxCutTiles) {
+    pl.ksplit = std::min(splits, pl.stages);
+    if (pl.ksplit >= 2) pl.dp_tiles = 0;
+  } else if (splits == 0 && pl.stages >= 2) {
+    const int waves = (tiles + cus - 1) / cus;
+    const double eff = (double)tiles / ((double)waves * cus);
+    if (eff < 0.92) {
+      const int dp = (tiles / cus) * cus;
+      const int rem = tiles - dp;
+      double best = (double)((rem + cus - 1) / cus);
+      int best_k = 1;
+      for (int k = 2; k <= std::min(pl.stages, 16); ++k) {
+        const double t = (double)(((int64_t)rem * k + cus - 1) / cus) / k + 0.01 * k;
+        if (t < best - 1e-9) {
+          best = t;
+          best_k = k;
+        }
+      }
+      if (best_k > 1 && rem <= kMaxCutTiles) {
+        pl.dp_tiles = dp;
+        pl.ksplit = best_k;
+      }
+    }
+  }
+  pl.grid = pl.dp_tiles + (tiles - pl.dp_tiles) * pl.ksplit;
+  pl.counter_bytes = QL_W4A16_COUNTER_BYTES;
+  pl.partial_bytes =
+      pl.dp_tiles < tiles ? (size_t)(tiles - pl.dp_tiles) * pl.ksplit * pl.BM * pl.BN * sizeof(float) : 0;
+  return pl;
+}
+
+size_t w4a16_ws_bytes(const W4A16Plan& pl) {
+  return pl.partial_bytes ? pl.counter_bytes + pl.partial_bytes : 0;
+}
+
+int check_w4a16_shape(int64_t M, int64_t N, int64_t K) {
+  if (M < 0 || N <= 0 || K < 32 || K % 32 != 0)
+    return fail(QL_ERR_SHAPE, "expected x [M, K], w_q4 [N, K/2], w_scale [N, K/32] with K %% 32 == 0, K >= 32, N > 0; "
+                "got M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
+  if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || K > INT32_MAX / 2)
+    return fail(QL_ERR_SHAPE, "dimension too large: M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
+  return QL_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* qlinear_last_error(void) { return g_last_error.c_str(); }
+
+int qlinear_abi_version(void) { return (1 << 16) | 0; }
+
+size_t qlinear_w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int splits, int device) {
+  if (check_w4a16_shape(M, N, K) != QL_OK || M == 0) return 0;
+  int cus = 0;
+  if (device_cus(device, &cus) != QL_OK) return 0;
+  return w4a16_ws_bytes(plan_w4a16(M, N, K, splits, cus));
+}
+
+int qlinear_w4a16_auto_splits(int64_t M, int64_t N, int64_t K, int device) {
+  if (int rc = check_w4a16_shape(M, N, K)) return -rc;
+  int cus = 0;
+  if (int rc = device_cus(device, &cus)) return -rc;
+  if (M == 0) return 1;
+  const W4A16Plan pl = plan_w4a16(M, N, K, 0, cus);
+  return pl.dp_tiles < pl.tiles_m * pl.tiles_n ? pl.ksplit : 1;
+}
+
+int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const void* w_q4, const float* w_scale,
+                       const void* bias, void* y, int64_t M, int64_t N, int64_t K, int splits, void* workspace,
+                       size_t workspace_bytes, void* stream) {
+  if (x_dtype != QL_BF16 && x_dtype != QL_F16)
+    return fail(QL_ERR_DTYPE, "x dtype %s (%d) unsupported, expected bfloat16 or float16", dtype_name(x_dtype), x_dtype);
+  if (out_dtype != QL_F32 && out_dtype != QL_F16 && out_dtype != QL_BF16)
+    return fail(QL_ERR_DTYPE, "out dtype %s (%d) unsupported, expected float32/float16/bfloat16", dtype_name(out_dtype),
+                out_dtype);
+  if (int rc = check_w4a16_shape(M, N, K)) return rc;
+  if (splits < 0 || splits > 64) return fail(QL_ERR_ARG, "splits must be in [0, 64], got %d", splits);
+  if (M == 0) return ok();
+  if (!x || !w_q4 || !w_scale || !y) return fail(QL_ERR_ARG, "null x / w_q4 / w_scale / y pointer");
+  if (!aligned16(x) || !aligned16(w_q4))
+    return fail(QL_ERR_ALIGN, "x and w_q4 must be 16-byte aligned (x=%p w_q4=%p)", x, w_q4);
+  int cus = 0;
+  if (int rc = device_cus(-1, &cus)) return rc;
+  const W4A16Plan pl = plan_w4a16(M, N, K, splits, cus);
+  const size_t need = w4a16_ws_bytes(pl);
+  if (need > 0 && (!workspace || workspace_bytes < need))
+    return fail(QL_ERR_WORKSPACE, "workspace of %zu bytes needed (M=%lld N=%lld K=%lld splits=%d), got %zu at %p", need,
+                (long long)M, (long long)N, (long long)K, splits, workspace_bytes, workspace);
+  if (need > 0 && !aligned16(workspace)) return fail(QL_ERR_ALIGN, "workspace must be 16-byte aligned");
+
+  W4A16Params p{};
+  p.x = x;
+  p.wq = w_q4;
+  p.ws = w_scale;
+  p.bias = bias;
+  p.y = y;
+  p.counters = need ? (uint32_t*)workspace : nullptr;
+  p.partial = need ? (float*)((char*)workspace + pl.counter_bytes) : nullptr;
+  p.M = (int)M;
+  p.N = (int)N;
+  p.K = (int)K;
+  p.out_dtype = out_dtype;
+  p.tiles_m = pl.tiles_m;
+  p.tiles_n = pl.tiles_n;
+  p.stages = pl.stages;
+  p.dp_tiles = pl.dp_tiles;
+  p.ksplit = pl.ksplit;
+  const hipError_t e = w4a16_launch(pl.cfg, x_dtype == QL_BF16, p, pl.grid, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(QL_ERR_LAUNCH, "w4a16 launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int qlinear_quantize_int4(int x_dtype, int rule, const void* x, void* packed, float* scale, int64_t rows,
+                          int64_t K, void* stream) {
+  if (x_dtype != QL_F32 && x_dtype != QL_F16 && x_dtype != QL_BF16)
+    return fail(QL_ERR_DTYPE, "unsupported dtype %s (%d), expected float32/float16/bfloat16", dtype_name(x_dtype),
+                x_dtype);
+  if (rule != 0 && rule != 1) return fail(QL_ERR_ARG, "rule must be 0 (amax / 7) or 1 (amax * (1/7)), got %d", rule);
+  if (rows < 0 || K < 32 || K % 32 != 0)
+    return fail(QL_ERR_SHAPE, "x must be [rows, K] with K %% 32 == 0, got [%lld, %lld]", (long long)rows, (long long)K);
+  if (rows == 0) return ok();
+  if (!x || !packed || !scale) return fail(QL_ERR_ARG, "null x / packed / scale pointer");
+  if (!aligned16(x) || !aligned16(packed)) return fail(QL_ERR_ALIGN, "x and packed must be 16-byte aligned");
+  const hipError_t e = quantize_int4_launch(x_dtype, rule, x, packed, scale, rows, K, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(QL_ERR_LAUNCH, "quantize_int4 launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int qlinear_quantize_int8_per_token(int x_dtype, const void* x, int8_t* q, float* scale, int64_t M, int64_t K,
+                                    void* stream) {
+  if (x_dtype != QL_F32 && x_dtype != QL_F16 && x_dtype != QL_BF16)
+    return fail(QL_ERR_DTYPE, "unsupported dtype %s (%d), expected float32/float16/bfloat16", dtype_name(x_dtype),
+                x_dtype);
+  if (M < 0 || K <= 0 || K > INT32_MAX / 2)
+    return fail(QL_ERR_SHAPE, "x must be [M, K] with K > 0, got [%lld, %lld]", (long long)M, (long long)K);
+  if (M == 0) return ok();
+  if (M > INT32_MAX) return fail(QL_ERR_SHAPE, "M=%lld too large", (long long)M);
+  if (!x || !q || !scale) return fail(QL_ERR_ARG, "null x / q / scale pointer");
+  const hipError_t e = quantize_int8_per_token_launch(x_dtype, x, q, scale, M, K, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(QL_ERR_LAUNCH, "quantize_int8_per_token launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int qlinear_w8a8_gemm(int out_dtype, const int8_t* xq, const float* x_scale, const int8_t* wq, const float* w_scale,
+                      const void* bias, void* y, int64_t M, int64_t N, int64_t K, void* stream) {
+  if (out_dtype != QL_F32 && out_dtype != QL_F16 && out_dtype != QL_BF16 && out_dtype != QL_I32)
+    return fail(QL_ERR_DTYPE, "out dtype %s (%d) unsupported, expected float32/float16/bfloat16/int32",
+                dtype_name(out_dtype), out_dtype);
+  if (M < 0 || N <= 0 || K < 64 || K % 64 != 0 || M > INT32_MAX / 2 || N > INT32_MAX / 2 || K > INT32_MAX / 2)
+    return fail(QL_ERR_SHAPE, "expected xq [M, K], wq [N, K] with K %% 64 == 0, N > 0; got M=%lld N=%lld K=%lld",
+                (long long)M, (long long)N, (long long)K);
+  if (M == 0) return ok();
+  if (!xq || !wq || !y) return fail(QL_ERR_ARG, "null xq / wq / y pointer");
+  if (out_dtype != QL_I32 && (!x_scale || !w_scale)) return fail(QL_ERR_ARG, "null x_scale / w_scale pointer");
+  if (!aligned16(xq) || !aligned16(wq)) return fail(QL_ERR_ALIGN, "xq and wq must be 16-byte aligned");
+  const int cfg = M <= 16 ? 3 : M <= 64 ? 2 : M <= 128 ? 1 : 0;
+  const W8A8Config& c = w8a8_config(cfg);
+  W8A8Params p{};
+  p.xq = xq;
+  p.sx = x_scale;
+  p.wq = wq;
+  p.sw = w_scale;
+  p.bias = bias;
+  p.y = y;
+  p.M = (int)M;
+  p.N = (int)N;
+  p.K = (int)K;
+  p.out_dtype = out_dtype;
+  p.tiles_m = (int)((M + c.BM - 1) / c.BM);
+  p.tiles_n = (int)((N + c.BN - 1) / c.BN);
+  p.stages = (int)((K + 255) / 256);
+  const hipError_t e = w8a8_launch(cfg, p, p.tiles_m * p.tiles_n, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(QL_ERR_LAUNCH, "w8a8 launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+}  // extern "C"

@@ -1,0 +1,130 @@
+// Shared device helpers for the gfx950 (CDNA4, wave64) quantized-linear kernels.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace qlinear {
+
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+enum DType { kF32 = 0, kF16 = 1, kBF16 = 2, kI32 = 3 };
+
+constexpr int kWave = 64;
+constexpr int kGroup = 32;  // int4 quant group along K (ops.py BLOCK = 32)
+
+// ---- scalar conversions ------------------------------------------------------------------
+__device__ __forceinline__ float bf16_bits_to_f32(uint32_t bits16) {
+  return __builtin_bit_cast(float, bits16 << 16);
+}
+__device__ __forceinline__ float f16_bits_to_f32(uint32_t bits16) {
+  return (float)__builtin_bit_cast(_Float16, (uint16_t)bits16);
+}
+// Round-to-nearest-even pack of two fp32 into one dword (v_cvt_pk_bf16_f32 / v_cvt_pk_f16_f32).
+__device__ __forceinline__ uint32_t pack2_bf16(float lo, float hi) {
+  bf16x2 v;
+  v[0] = (__bf16)lo;
+  v[1] = (__bf16)hi;
+  return __builtin_bit_cast(uint32_t, v);
+}
+__device__ __forceinline__ uint32_t pack2_f16(float lo, float hi) {
+  f16x2 v;
+  v[0] = (_Float16)lo;
+  v[1] = (_Float16)hi;
+  return __builtin_bit_cast(uint32_t, v);
+}
+
+// Read element i of a buffer of dtype code dt as fp32.
+__device__ __forceinline__ float read_elem(const void* p, int dt, size_t i) {
+  if (dt == kF32) return ((const float*)p)[i];
+  const uint32_t b = ((const uint16_t*)p)[i];
+  return dt == kBF16 ? bf16_bits_to_f32(b) : f16_bits_to_f32(b);
+}
+
+// Write fp32 v as dtype dt (RNE) to element i.
+__device__ __forceinline__ void write_elem(void* p, int dt, size_t i, float v) {
+  if (dt == kF32) {
+    ((float*)p)[i] = v;
+  } else if (dt == kBF16) {
+    ((__bf16*)p)[i] = (__bf16)v;
+  } else {
+    ((_Float16*)p)[i] = (_Float16)v;
+  }
+}
+
+// ---- int4 -> 16-bit dequant in registers ---------------------------------------------------
+// One packed dword holds 8 consecutive K elements: nibble t (bits 4t..4t+3) is element t,
+// two's complement (the reference's packing, ops.py:119-121). Returns the 8 values q*s
+// rounded to bf16/fp16, natural order, two per dword (element 2b in the low half of dword b).
+// u = nibble ^ 8 = q + 8 is exact as a byte; fmaf(u, s, -8s) = q*s rounded once in fp32
+// (the product is exact inside the FMA and -8s is exact), then one RNE rounding to 16 bits.
+template <bool kBf16>
+__device__ __forceinline__ u32x4 dequant8(uint32_t w, float s, float neg8s) {
+  const uint32_t ev = (w & 0x0F0F0F0Fu) ^ 0x08080808u;         // bytes: u0 u2 u4 u6
+  const uint32_t od = ((w >> 4) & 0x0F0F0F0Fu) ^ 0x08080808u;  // bytes: u1 u3 u5 u7
+  u32x4 r;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const float lo = fmaf((float)((ev >> (8 * b)) & 0xFFu), s, neg8s);
+    const float hi = fmaf((float)((od >> (8 * b)) & 0xFFu), s, neg8s);
+    r[b] = kBf16 ? pack2_bf16(lo, hi) : pack2_f16(lo, hi);
+  }
+  return r;
+}
+
+// ---- MFMA wrappers (v_mfma_f32_16x16x32_{bf16,f16}, v_mfma_i32_16x16x64_i8) ----------------
+// Operand layout (lane l of 64): A supplies row l%16, B supplies column l%16, each with the
+// 8 (16-bit) or 16 (int8) K values of K-slot block l/16; D lane l holds column l%16,
+// rows 4*(l/16) + 0..3. The kernels only rely on A and B using the same K-slot map.
+template <bool kBf16>
+__device__ __forceinline__ f32x4 mfma16(u32x4 a, u32x4 b, f32x4 c) {
+  if constexpr (kBf16) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8, a),
+                                                  __builtin_bit_cast(bf16x8, b), c, 0, 0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a),
+                                                 __builtin_bit_cast(f16x8, b), c, 0, 0, 0);
+  }
+}
+__device__ __forceinline__ i32x4 mfma16_i8(u32x4 a, u32x4 b, i32x4 c) {
+  return __builtin_amdgcn_mfma_i32_16x16x64_i8(__builtin_bit_cast(i32x4, a),
+                                              __builtin_bit_cast(i32x4, b), c, 0, 0, 0);
+}
+
+// ---- direct global -> LDS 16-byte loads (global_load_lds_dwordx4) ----------------------------
+// Lane i of the wave writes its 16 bytes to lds_base + 16*i; lds_base must be wave-uniform.
+__device__ __forceinline__ void load_lds16(const void* gptr, void* lds_base) {
+  __builtin_amdgcn_global_load_lds(gptr, (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
+}
+__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+
+// ---- workgroup -> tile order ---------------------------------------------------------------
+// Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2). Renumber them
+// so that consecutive logical ids run on the same XCD and share A/B panels in its L2.
+__device__ __forceinline__ int xcd_remap(int g, int G) {
+  constexpr int kXcd = 8;
+  const int xcd = g % kXcd, local = g / kXcd;
+  const int per = G / kXcd, rem = G % kXcd;
+  return xcd < rem ? xcd * (per + 1) + local : rem * (per + 1) + (xcd - rem) * per + local;
+}
+
+// Grouped ("super-tile") order: kGroupM tile-rows walk the N tiles together.
+__device__ __forceinline__ void tile_coords(int t, int tiles_m, int tiles_n, int group_m, int& tm,
+                                            int& tn) {
+  const int per_group = group_m * tiles_n;
+  const int grp = t / per_group;
+  const int first_m = grp * group_m;
+  const int gsize = min(tiles_m - first_m, group_m);
+  const int r = t - grp * per_group;
+  tm = first_m + r % gsize;
+  tn = r / gsize;
+}
+
+}  // namespace qlinear

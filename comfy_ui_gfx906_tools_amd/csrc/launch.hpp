@@ -1,0 +1,57 @@
+// Host-side launch interface between the C ABI (capi.cpp) and the kernel files.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stddef.h>
+#include <stdint.h>
+
+namespace qlinear {
+
+struct W4A16Params {
+  const void* x;         // [M, K] bf16 / fp16
+  const void* wq;        // [N, K/2] packed int4
+  const float* ws;       // [N, K/32]
+  const void* bias;      // [N] out dtype, or null
+  void* y;               // [M, N] out dtype
+  float* partial;        // partial tiles: (tiles - dp_tiles) * ksplit slots of BM * BN fp32
+  uint32_t* counters;    // one per cut tile (tile - dp_tiles), zero between calls
+  int M, N, K;
+  int out_dtype;
+  int tiles_m, tiles_n;
+  int stages;            // ceil(K / 256): steps of two 128-K pipeline stages
+  int dp_tiles;          // tiles processed whole, one workgroup each
+  int ksplit;            // K pieces of every tile past dp_tiles (>= 2 when any)
+};
+
+struct W4A16Config {
+  int id, BM, BN;
+};
+
+const W4A16Config& w4a16_config(int id);
+hipError_t w4a16_launch(int cfg, bool bf16, const W4A16Params& p, int grid, hipStream_t stream);
+
+struct W8A8Params {
+  const int8_t* xq;      // [M, K]
+  const float* sx;       // [M]
+  const int8_t* wq;      // [N, K]
+  const float* sw;       // [N]
+  const void* bias;      // [N] out dtype, or null
+  void* y;               // [M, N]
+  int M, N, K;
+  int out_dtype;         // kF32 / kF16 / kBF16 / kI32
+  int tiles_m, tiles_n;
+  int stages;            // K / 256
+};
+
+struct W8A8Config {
+  int id, BM, BN;
+};
+const W8A8Config& w8a8_config(int id);
+hipError_t w8a8_launch(int cfg, const W8A8Params& p, int grid, hipStream_t stream);
+
+hipError_t quantize_int4_launch(int dtype, int rule, const void* x, void* packed, float* scale,
+                                int64_t rows, int64_t K, hipStream_t stream);
+hipError_t quantize_int8_per_token_launch(int dtype, const void* x, int8_t* q, float* scale,
+                                          int64_t M, int64_t K, hipStream_t stream);
+
+}  // namespace qlinear

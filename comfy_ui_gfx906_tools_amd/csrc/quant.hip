@@ -1,0 +1,138 @@
+// Quantizer kernels for gfx950.
+//
+// quantize_int4: symmetric block-32 int4 with the reference's packing
+//   (nodes/ComfyUI-Gfx906Int4/ops.py:108-126: scale = clamp_min(amax, 1e-8) / 7,
+//   codes = clamp(round_half_even(x / scale), -8, 7), byte j = code[2j] | code[2j+1] << 4).
+//   rule 0 divides the amax by 7 (torch on CPU), rule 1 multiplies by fl(1/7) (torch's
+//   scalar-divisor path on GPU and csrc/int4_gemm_scaled.hip:210-211). One thread per block.
+// quantize_int8_per_token: s = max(amax(row), 1e-8) * fl(1/127),
+//   q = clamp(rint(x / s), -127, 127) (csrc/int8_gemm.hip:215-246, block widened to the row).
+//   One 256-thread workgroup per row.
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace qlinear {
+
+namespace {
+
+constexpr int kQThreads = 256;
+
+template <int DT>
+__device__ __forceinline__ void load32(const void* x, size_t base, float (&v)[32]) {
+  if constexpr (DT == kF32) {
+    const u32x4* p = (const u32x4*)((const float*)x + base);
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const u32x4 w = p[c];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        // copy the element out first: bit_cast of a vector subscript reads the vector's first bytes
+        const uint32_t bits = w[e];
+        v[4 * c + e] = __builtin_bit_cast(float, bits);
+      }
+    }
+  } else {
+    const u32x4* p = (const u32x4*)((const uint16_t*)x + base);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const u32x4 w = p[c];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t lo = w[e] & 0xFFFFu, hi = w[e] >> 16;
+        v[8 * c + 2 * e] = DT == kBF16 ? bf16_bits_to_f32(lo) : f16_bits_to_f32(lo);
+        v[8 * c + 2 * e + 1] = DT == kBF16 ? bf16_bits_to_f32(hi) : f16_bits_to_f32(hi);
+      }
+    }
+  }
+}
+
+template <int DT>
+__global__ __launch_bounds__(kQThreads) void quantize_int4_kernel(const void* __restrict__ x,
+                                                                  u32x4* __restrict__ packed,
+                                                                  float* __restrict__ scale,
+                                                                  long long blocks, int rule) {
+  const long long b = (long long)blockIdx.x * kQThreads + threadIdx.x;
+  if (b >= blocks) return;
+  float v[32];
+  load32<DT>(x, (size_t)b * 32, v);
+  float amax = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 32; ++e) amax = fmaxf(amax, fabsf(v[e]));
+  amax = fmaxf(amax, 1e-8f);
+  const float s = rule == 0 ? __fdiv_rn(amax, 7.0f) : __fmul_rn(amax, 1.0f / 7.0f);
+  u32x4 out = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int e = 0; e < 32; ++e) {
+    const float q = fminf(fmaxf(rintf(__fdiv_rn(v[e], s)), -8.0f), 7.0f);
+    out[e / 8] |= ((uint32_t)(int)q & 0xFu) << (4 * (e % 8));
+  }
+  packed[b] = out;
+  scale[b] = s;
+}
+
+template <int DT>
+__global__ __launch_bounds__(kQThreads) void quantize_int8_row_kernel(const void* __restrict__ x,
+                                                                      int8_t* __restrict__ q,
+                                                                      float* __restrict__ scale,
+                                                                      int K) {
+  __shared__ float red[kQThreads / kWave];
+  const int row = blockIdx.x;
+  const size_t base = (size_t)row * K;
+  float amax = 0.0f;
+  for (int k = threadIdx.x; k < K; k += kQThreads) amax = fmaxf(amax, fabsf(read_elem(x, DT, base + k)));
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, kWave));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  amax = red[0];
+#pragma unroll
+  for (int w = 1; w < kQThreads / kWave; ++w) amax = fmaxf(amax, red[w]);
+  const float s = __fmul_rn(fmaxf(amax, 1e-8f), 1.0f / 127.0f);
+  if (threadIdx.x == 0) scale[row] = s;
+  for (int k = threadIdx.x; k < K; k += kQThreads) {
+    const float v = read_elem(x, DT, base + k);
+    q[base + k] = (int8_t)(int)fminf(fmaxf(rintf(__fdiv_rn(v, s)), -127.0f), 127.0f);
+  }
+}
+
+}  // namespace
+
+hipError_t quantize_int4_launch(int dtype, int rule, const void* x, void* packed, float* scale,
+                                int64_t rows, int64_t K, hipStream_t stream) {
+  const long long blocks = (long long)rows * (K / 32);
+  const dim3 grid((unsigned)((blocks + kQThreads - 1) / kQThreads));
+  switch (dtype) {
+    case kF32:
+      hipLaunchKernelGGL(quantize_int4_kernel<kF32>, grid, dim3(kQThreads), 0, stream, x, (u32x4*)packed,
+                         scale, blocks, rule);
+      break;
+    case kF16:
+      hipLaunchKernelGGL(quantize_int4_kernel<kF16>, grid, dim3(kQThreads), 0, stream, x, (u32x4*)packed,
+                         scale, blocks, rule);
+      break;
+    default:
+      hipLaunchKernelGGL(quantize_int4_kernel<kBF16>, grid, dim3(kQThreads), 0, stream, x, (u32x4*)packed,
+                         scale, blocks, rule);
+      break;
+  }
+  return hipGetLastError();
+}
+
+hipError_t quantize_int8_per_token_launch(int dtype, const void* x, int8_t* q, float* scale, int64_t M,
+                                          int64_t K, hipStream_t stream) {
+  const dim3 grid((unsigned)M);
+  switch (dtype) {
+    case kF32:
+      hipLaunchKernelGGL(quantize_int8_row_kernel<kF32>, grid, dim3(kQThreads), 0, stream, x, q, scale, (int)K);
+      break;
+    case kF16:
+      hipLaunchKernelGGL(quantize_int8_row_kernel<kF16>, grid, dim3(kQThreads), 0, stream, x, q, scale, (int)K);
+      break;
+    default:
+      hipLaunchKernelGGL(quantize_int8_row_kernel<kBF16>, grid, dim3(kQThreads), 0, stream, x, q, scale, (int)K);
+      break;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace qlinear

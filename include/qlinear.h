@@ -1,0 +1,117 @@
+/*
+ * qlinear.h -- C ABI of libqlinear.so, the gfx950 (MI355X) quantized-linear engine.
+ *
+ * Plain pointers, sizes and an opaque stream. The library never allocates or frees:
+ * every buffer, workspace included, is passed in by the caller (PyTorch's caching
+ * allocator on the Python side), and every launch goes on the caller's HIP stream.
+ *
+ * Return value of every entry point: 0 (QL_OK) or one of the QL_ERR_* codes below;
+ * qlinear_last_error() then returns a message naming expected vs actual, kept per host
+ * thread. Entry points are re-entrant and keep no global mutable state beyond a
+ * per-device, lock-protected cache of the CU count.
+ *
+ * Layouts shared with the reference (luna-niemitalo/comfy_ui_gfx906_tools):
+ *   packed int4 weight  int8  [N, K/2]  byte j of a row = code[2j] & 0xF | (code[2j+1] & 0xF) << 4,
+ *                                       codes two's complement in [-8, 7]
+ *                                       (nodes/ComfyUI-Gfx906Int4/ops.py:108-126)
+ *   group scales        fp32  [N, K/32] one scale per 32 consecutive K elements (ops.py:215)
+ *   dtype codes         0 = fp32, 1 = fp16, 2 = bf16 (csrc/binding.cpp:45-50); 3 = int32 is an
+ *                       output-only code of this library (raw W8A8 accumulators)
+ * All row-major, rows contiguous; pointers 16-byte aligned.
+ */
+#ifndef QLINEAR_H
+#define QLINEAR_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+enum qlinear_dtype { QL_F32 = 0, QL_F16 = 1, QL_BF16 = 2, QL_I32 = 3 };
+
+enum qlinear_status {
+  QL_OK = 0,
+  QL_ERR_ARG = 1,       /* null pointer, bad enum, bad option */
+  QL_ERR_SHAPE = 2,     /* sizes inconsistent or out of the supported range */
+  QL_ERR_DTYPE = 3,     /* dtype not supported for this operand */
+  QL_ERR_ALIGN = 4,     /* pointer not 16-byte aligned */
+  QL_ERR_WORKSPACE = 5, /* workspace missing or too small */
+  QL_ERR_LAUNCH = 6,    /* HIP runtime error at launch */
+  QL_ERR_DEVICE = 7     /* HIP device query failed */
+};
+
+/* Message for the last failing call on this host thread ("" if none). */
+const char* qlinear_last_error(void);
+
+/* ABI version of this header: (major << 16) | minor. */
+int qlinear_abi_version(void);
+
+/* ---------------------------------------------------------------------------------------
+ * W4A16 linear: y[M,N] = x[M,K] @ dequant(w_q4, w_scale)^T (+ bias[N]).
+ * Replaces the pair ext.quantize_int4 + ext.gemm_int4 that int4_linear calls
+ * (nodes/ComfyUI-Gfx906Int4/ops.py:181-182; csrc/binding.cpp:53-112; dispatchers
+ * csrc/int4_gemm_scaled.hip:248-269): the activation is not quantized here, the weight is
+ * dequantized in registers and fed to bf16/fp16 MFMA with fp32 accumulation.
+ *   x_dtype   QL_BF16 or QL_F16 (the MFMA operand type)
+ *   out_dtype QL_F32, QL_F16 or QL_BF16; bias (optional, may be NULL) has dtype out_dtype
+ *   K % 32 == 0, K >= 32; M >= 0 (M == 0 launches nothing)
+ *   splits    0 = automatic (the engine picks split-K / stream-K for under-filled grids),
+ *             1 = one workgroup per output tile, 2..64 = that many workgroups per tile.
+ *   workspace device memory of qlinear_w4a16_workspace_bytes(...) bytes whose first
+ *             QL_W4A16_COUNTER_BYTES bytes were zeroed once when it was allocated (the kernels
+ *             leave them zero again); may be NULL when that size is 0. Calls sharing one
+ *             workspace must be ordered (same stream).
+ * ------------------------------------------------------------------------------------- */
+#define QL_W4A16_COUNTER_BYTES 65536u /* fixed: counters of at most 16384 cut tiles */
+
+size_t qlinear_w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int splits, int device);
+
+int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const void* w_q4,
+                       const float* w_scale, const void* bias, void* y, int64_t M, int64_t N,
+                       int64_t K, int splits, void* workspace, size_t workspace_bytes,
+                       void* stream);
+
+/* Number of workgroups per output tile that splits == 0 resolves to; mirrors
+ * ext.gemm_int4_auto_splits (csrc/binding.cpp:36-43, 359-362). */
+int qlinear_w4a16_auto_splits(int64_t M, int64_t N, int64_t K, int device);
+
+/* ---------------------------------------------------------------------------------------
+ * Symmetric block-32 int4 quantize + pack of a float matrix x[rows, K] (fp32/fp16/bf16):
+ *   scale = max(amax(block), 1e-8) / 7      (rule 0, torch on CPU: ops.py:115-116)
+ *   scale = max(amax(block), 1e-8) * (1/7)  (rule 1, torch on GPU and the reference's own
+ *                                            kernel: csrc/int4_gemm_scaled.hip:210-211)
+ *   code  = clamp(rint(x / scale), -8, 7), packed two per byte as above.
+ * Replaces quantize_pack_int4 (ops.py:108-126) for device-resident weights, and
+ * quantize_int4_dispatch (csrc/int4_gemm_scaled.hip:248-252) for activations.
+ * ------------------------------------------------------------------------------------- */
+int qlinear_quantize_int4(int x_dtype, int rule, const void* x, void* packed, float* scale,
+                          int64_t rows, int64_t K, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * Per-token int8 quantize of activations x[M,K] (fp32/fp16/bf16):
+ *   s[m] = max(amax(row m), 1e-8) * (1/127); q = clamp(rint(x / s), -127, 127)
+ * The reference's int8 rule (csrc/int8_gemm.hip:215-246, quantize_int8_dispatch :280) with
+ * the block widened from 32 to the whole row.
+ * ------------------------------------------------------------------------------------- */
+int qlinear_quantize_int8_per_token(int x_dtype, const void* x, int8_t* q, float* scale,
+                                    int64_t M, int64_t K, void* stream);
+
+/* ---------------------------------------------------------------------------------------
+ * W8A8 linear: acc[m,n] = sum_k xq[m,k] * wq[n,k] in int32 (exact), then
+ *   y = float(acc) * (x_scale[m] * w_scale[n]) (+ bias[n]), each step rounded in fp32,
+ * the scale-product order of csrc/int8_gemm.hip:191-193, 209. out_dtype QL_I32 stores the
+ * raw accumulators (x_scale, w_scale and bias are then ignored). K % 64 == 0.
+ * Counterpart of gemm_int8_dispatch (csrc/int8_gemm.hip:287-295) with per-token x
+ * per-channel scales instead of block-32 scales.
+ * ------------------------------------------------------------------------------------- */
+int qlinear_w8a8_gemm(int out_dtype, const int8_t* xq, const float* x_scale, const int8_t* wq,
+                      const float* w_scale, const void* bias, void* y, int64_t M, int64_t N,
+                      int64_t K, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* QLINEAR_H */

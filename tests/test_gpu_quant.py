@@ -1,0 +1,58 @@
+"""Device-side int4 quantize + pack (quantize_pack_int4 for GPU-resident weights): bit-exact
+against the oracle for both scale rules, and against the reference's own torch expression
+(ops.py:108-126) evaluated by torch on the same GPU."""
+import numpy as np
+import pytest
+import torch
+
+from oracle import qlinear_oracle as orc
+from tests.gpu_util import to_np_f32
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def _lib():
+    from comfy_ui_gfx906_tools_amd import _lib
+    return _lib
+
+
+def _reference_torch_expression(t: torch.Tensor):
+    """ops.py:108-126 verbatim in its arithmetic (the reference's quantizer), run by torch."""
+    K = t.shape[-1]
+    tb = t.reshape(-1, K // 32, 32).float()
+    amax = tb.abs().amax(dim=-1, keepdim=True).clamp_min(1e-8)
+    scale = amax / 7.0
+    codes = torch.round(tb / scale).clamp(-8, 7).to(torch.int32).reshape(-1, K)
+    packed = ((codes[:, 0::2] & 0xF) | ((codes[:, 1::2] & 0xF) << 4)).to(torch.uint8).view(torch.int8)
+    return packed.reshape(*t.shape[:-1], K // 2), scale.reshape(*t.shape[:-1], K // 32)
+
+
+@pytest.mark.parametrize("rule,rname", [(0, "div"), (1, "recip")])
+@pytest.mark.parametrize("dt", [torch.float32, torch.bfloat16, torch.float16])
+def test_quantize_int4_matches_oracle(rule, rname, dt):
+    print(f"case quant4 rule={rname} {dt}", flush=True)
+    g = torch.Generator().manual_seed(7)
+    x = (torch.randn(67, 1024, generator=g) * torch.rand(67, 1, generator=g) * 3).to(dt)
+    x[3] = 0
+    p, s = _lib().quantize_int4(x.to(DEV), rule)
+    p_ref, s_ref = orc.quantize_pack_int4(to_np_f32(x), rule=rname)
+    assert np.array_equal(s.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+    assert np.array_equal(p.cpu().numpy(), p_ref)
+
+
+def test_quantize_pack_int4_gpu_equals_reference_torch_on_gpu():
+    """ops.quantize_pack_int4 of a device tensor must equal the reference's torch expression
+    evaluated on the same device, bit for bit (packed bytes and scales)."""
+    from comfy_ui_gfx906_tools_amd import ops
+    g = torch.Generator().manual_seed(8)
+    w = (torch.randn(512, 3072, generator=g) * 0.02).to(DEV)
+    p, s = ops.quantize_pack_int4(w)
+    p_ref, s_ref = _reference_torch_expression(w)
+    same_scale = torch.equal(s, s_ref)
+    # report which rule torch used on this device if the HIP rule disagrees
+    if not same_scale:
+        p0, s0 = _lib().quantize_int4(w, 0)
+        p1, s1 = _lib().quantize_int4(w, 1)
+        pytest.fail(f"scale mismatch: torch-GPU == rule0? {torch.equal(s0, s_ref)}; == rule1? {torch.equal(s1, s_ref)}")
+    assert torch.equal(p, p_ref)

@@ -1,0 +1,134 @@
+"""W4A16 parity on the GPU: the gfx950 kernel vs the CPU oracle (small shapes, golden fixture)
+and vs an fp32 torch GEMM of the dequantized weight (the BASELINE configs at full size).
+
+Tolerance: max|y - ref| / max|ref| <= 2e-3 against the fp32-dequant
+reference with fp32 output. With 16-bit output the kernel's value is rounded once more, so
+bf16/fp16 outputs are gated elementwise at |y - round(ref)| <= 1 ulp(round(ref)) + 2e-3*max|ref|.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import qlinear_oracle as orc
+from tests.conftest import golden_path
+from tests.gpu_util import bf16_ulp, dequant_torch, f16_ulp, rel_max_err, seeded_linear, to_np_f32
+
+pytestmark = pytest.mark.gpu
+TOL = 2e-3
+DEV = "cuda:0"
+
+
+def _lib():
+    from comfy_ui_gfx906_tools_amd import _lib
+    return _lib
+
+
+def _run(x, wq, ws, bias=None, out_dtype=torch.float32, splits=0):
+    return _lib().w4a16_gemm(x.to(DEV), wq.to(DEV), ws.to(DEV), None if bias is None else bias.to(DEV),
+                             out_dtype=out_dtype, splits=splits)
+
+
+SMALL = [
+    # M, N, K, x dtype, bias
+    (1, 256, 256, torch.bfloat16, False),
+    (5, 300, 96, torch.bfloat16, True),
+    (16, 512, 1024, torch.float16, False),
+    (17, 512, 1024, torch.float16, True),
+    (64, 256, 512, torch.bfloat16, True),
+    (100, 700, 160, torch.bfloat16, False),
+    (300, 1000, 4096, torch.bfloat16, True),
+    (513, 384, 3072, torch.float16, False),
+]
+
+
+@pytest.mark.parametrize("M,N,K,xdt,with_bias", SMALL)
+def test_w4a16_vs_oracle_fp32_out(M, N, K, xdt, with_bias):
+    print(f"case M={M} N={N} K={K} x={xdt} bias={with_bias}", flush=True)
+    x, wq, ws = seeded_linear(M, N, K, seed=M * 7 + N + K, x_dtype=xdt)
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(1)) if with_bias else None
+    y = to_np_f32(_run(x, wq, ws, bias))
+    ref = orc.w4a16_reference(to_np_f32(x), wq.numpy(), ws.numpy(), None if bias is None else bias.numpy())
+    assert y.shape == (M, N)
+    assert np.isfinite(y).all()
+    err = rel_max_err(y, ref)
+    assert err <= TOL, f"max rel err {err:.3e} > {TOL}"
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
+def test_w4a16_16bit_out(out_dtype, xdt):
+    M, N, K = 96, 640, 2048
+    print(f"case 16-bit out {out_dtype} x={xdt}", flush=True)
+    x, wq, ws = seeded_linear(M, N, K, seed=11, x_dtype=xdt)
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(2)).to(out_dtype)
+    y = to_np_f32(_run(x, wq, ws, bias, out_dtype=out_dtype))
+    ref = orc.w4a16_reference(to_np_f32(x), wq.numpy(), ws.numpy(), to_np_f32(bias)).astype(np.float32)
+    name = "bfloat16" if out_dtype == torch.bfloat16 else "float16"
+    ref_r = orc.round_to_dtype(ref, name)
+    ulp = bf16_ulp(ref_r) if out_dtype == torch.bfloat16 else f16_ulp(ref_r)
+    bound = ulp + TOL * np.abs(ref).max()
+    assert (np.abs(y - ref_r) <= bound).all(), f"max excess {(np.abs(y - ref_r) - bound).max():.3e}"
+
+
+@pytest.mark.parametrize("splits", [1, 2, 3, 7])
+def test_w4a16_split_k_and_determinism(splits):
+    M, N, K = 200, 512, 2048
+    print(f"case splits={splits}", flush=True)
+    x, wq, ws = seeded_linear(M, N, K, seed=5)
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(3))
+    y1 = _run(x, wq, ws, bias, splits=splits)
+    y2 = _run(x, wq, ws, bias, splits=splits)
+    assert torch.equal(y1, y2), "split-K result is not deterministic"
+    ref = orc.w4a16_reference(to_np_f32(x), wq.numpy(), ws.numpy(), bias.numpy())
+    assert rel_max_err(to_np_f32(y1), ref) <= TOL
+
+
+def test_w4a16_exact_on_integer_grid():
+    """Integer x in [-4, 4], codes in [-8, 7], power-of-two scales >= 2^-6, K = 256: every
+    dequantized weight is exact in bf16 and every partial sum is a multiple of 2^-6 below 2^12,
+    exact in fp32. The kernel must then equal the float64 oracle exactly."""
+    M, N, K = 40, 300, 256
+    g = np.random.default_rng(9)
+    x = torch.from_numpy(g.integers(-4, 5, (M, K)).astype(np.float32)).to(torch.bfloat16)
+    codes = g.integers(-8, 8, (N, K))
+    nib = (codes & 0xF).astype(np.uint8)
+    packed = (nib[:, 0::2] | (nib[:, 1::2] << 4)).view(np.int8)
+    scale = (2.0 ** g.integers(-6, 0, (N, K // 32))).astype(np.float32)
+    y = to_np_f32(_run(x, torch.from_numpy(packed), torch.from_numpy(scale)))
+    ref = orc.w4a16_reference(to_np_f32(x), packed, scale)
+    assert np.array_equal(y.astype(np.float64), ref), f"max abs diff {np.abs(y - ref).max()}"
+
+
+def test_w4a16_golden_fixture():
+    """Committed seeded case (tests/golden/w4a16_small.npz, written by make_golden.py from the
+    oracle): the kernel must reproduce the stored fp64 reference within the gate."""
+    d = np.load(golden_path("w4a16_small.npz"))
+    x = torch.from_numpy(orc.bf16_bits_to_f32(d["x_bf16_bits"])).to(torch.bfloat16)
+    y = to_np_f32(_run(x, torch.from_numpy(d["w_q4"]), torch.from_numpy(d["w_scale"]),
+                       torch.from_numpy(d["bias"])))
+    assert rel_max_err(y, d["y_ref"]) <= TOL
+
+
+@pytest.mark.parametrize("M,K,N,xdt", [
+    (4608, 3072, 3072, torch.float16),    # C1 shape
+    (4608, 3072, 12288, torch.bfloat16),  # C2 fc1
+    (4608, 12288, 3072, torch.bfloat16),  # C2 fc2
+    (1, 4096, 10240, torch.bfloat16),     # C4 skinny
+    (16, 4096, 10240, torch.bfloat16),
+    (64, 4096, 10240, torch.bfloat16),
+    (256, 4096, 10240, torch.bfloat16),
+    (1, 3072, 18432, torch.bfloat16),     # C4 modulation
+])
+def test_w4a16_baseline_shapes_vs_torch_fp32(M, K, N, xdt):
+    """Full-size BASELINE shapes against torch's fp32 GEMM of the fp32-dequantized weight (GPU)."""
+    print(f"case full-size M={M} K={K} N={N}", flush=True)
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(M, K, generator=g).to(xdt).to(DEV)
+    w = (torch.randn(N, K, generator=g) * 0.02).to(DEV)
+    from comfy_ui_gfx906_tools_amd import ops
+    wq, ws = ops.quantize_pack_int4(w)
+    y = _lib().w4a16_gemm(x, wq, ws, out_dtype=torch.float32)
+    ref = x.float() @ dequant_torch(wq, ws).t()
+    err = ((y - ref).abs().max() / ref.abs().max()).item()
+    del w
+    assert err <= TOL, f"max rel err {err:.3e}"
