@@ -1,0 +1,204 @@
+#!/usr/bin/env python3
+"""Benchmark of the W4A16 hot path on one MI355X: the Flux-style DiT MLP pair.
+
+One step = fc1 3072->12288 (W4A16, bias) -> GELU-tanh -> fc2 12288->3072 (W4A16, bias) over
+M = 4608 tokens (4096 image + 512 text), bf16 activations, int4 group-32 weights in the
+reference's packed layout, random init (seed 1 = config index), inputs resident in HBM.
+Each linear is the engine's fp16 route: the exact row-scaled fp16 staging pass, then the W4A16
+GEMM kernel. Prints ONE JSON line (the driver's contract) with the whole-step TFLOP/s (2*M*N*K per
+GEMM; GELU and staging not counted as flops), the GEMM kernel's MFMA roofline from HIP events
+around its launches, the parity gate of this same run, and the CPU baseline (the oracle's fp32
+dequant-then-matmul path on the host cores).
+
+Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16/fp16 MFMA, AMD spec
+HERE = os.path.dirname(os.path.abspath(__file__))
+M_TOKENS, HIDDEN, MLP = 4608, 3072, 12288
+GATE = 2e-3
+
+
+def parse():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--cpu-repeats", type=int, default=3)
+    return ap.parse_args()
+
+
+def gelu_tanh_np(h):
+    import numpy as np
+    return 0.5 * h * (1.0 + np.tanh(np.float32(0.7978845608028654) * (h + np.float32(0.044715) * h * h * h)))
+
+
+def cpu_baseline(x_bf16, w1, s1, b1, w2, s2, b2, repeats):
+    """The oracle's CPU path (port of the reference's dequantize-then-matmul W4A16, nodes.py:43-52
+    + stock matmul), fp32, timed on the whole C2 step: weights dequantized once (outside the
+    timing, like Gfx906Int4Patch does at patch time), then per step matmul -> GELU -> matmul.
+    Best of `repeats`."""
+    import numpy as np
+    sys.path.insert(0, HERE)
+    from oracle import qlinear_oracle as orc
+    try:
+        from threadpoolctl import threadpool_info
+        threads = max([p.get("num_threads", 1) for p in threadpool_info() if p.get("user_api") == "blas"] or [1])
+    except Exception:
+        threads = os.cpu_count() or 1
+    x = orc.bf16_bits_to_f32(x_bf16)
+    W1 = orc.dequant_int4(w1, s1)
+    W2 = orc.dequant_int4(w2, s2)
+    best = float("inf")
+    for _ in range(repeats):
+        t0 = time.perf_counter()
+        h = x @ W1.T + b1
+        h = gelu_tanh_np(h).astype(np.float32)
+        y = h @ W2.T + b2
+        best = min(best, time.perf_counter() - t0)
+    flops = 2.0 * M_TOKENS * HIDDEN * MLP * 2
+    return {"value": round(flops / best / 1e12, 4), "unit": "TFLOP/s", "cores": int(threads), "kind": "port",
+            "sample": f"full C2 step on the host (M={M_TOKENS}, fp32 numpy BLAS, dequant outside the timing), "
+                      f"best of {repeats}: {best:.2f} s/step", "_check": float(np.abs(y).max())}
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU: the W4A16 path is measured on a single MI355X; "
+                                   "multi-GPU sharding is described in DESIGN.md and not launched",
+                          "n_gpus": args.gpus}))
+        sys.exit(2)
+    import numpy as np
+    import torch
+    sys.path.insert(0, HERE)
+    from comfy_ui_gfx906_tools_amd import _lib, ops
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    _lib.load_library()
+
+    # ---- synthetic C2 inputs (seed 1 = config index), generated on the GPU -------------------
+    g = torch.Generator(device=dev).manual_seed(1)
+    x = torch.randn(M_TOKENS, HIDDEN, device=dev, generator=g).to(torch.bfloat16)
+    w1f = torch.randn(MLP, HIDDEN, device=dev, generator=g) * 0.02
+    w2f = torch.randn(HIDDEN, MLP, device=dev, generator=g) * 0.02
+    b1 = (torch.randn(MLP, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    b2 = (torch.randn(HIDDEN, device=dev, generator=g) * 0.02).to(torch.bfloat16)
+    w1q, w1s = ops.quantize_pack_int4(w1f)  # the reference's quantizer rule, on the device
+    w2q, w2s = ops.quantize_pack_int4(w2f)
+    del w1f, w2f
+
+    gemm_events = []
+
+    def linear(a, wq, ws, bias, record):
+        a16, rs = _lib.rows_to_f16(a)
+        if record:
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+        y = _lib.w4a16_gemm(a16, wq, ws, bias, out_dtype=torch.bfloat16, row_scale=rs)
+        if record:
+            e1.record()
+            gemm_events.append((e0, e1))
+        return y
+
+    def step(record=False):
+        h = linear(x, w1q, w1s, b1, record)
+        h = torch.nn.functional.gelu(h, approximate="tanh")
+        return linear(h, w2q, w2s, b2, record)
+
+    # ---- parity gate of this run (fp32-dequant reference on the GPU, BASELINE tolerance) -----
+    x16a, rsa = _lib.rows_to_f16(x)
+    h32 = _lib.w4a16_gemm(x16a, w1q, w1s, b1.float(), out_dtype=torch.float32, row_scale=rsa)
+    ref1 = x.float() @ dequant_fp32(w1q, w1s).t() + b1.float()
+    err1 = ((h32 - ref1).abs().max() / ref1.abs().max()).item()
+    hg = torch.nn.functional.gelu(h32.to(torch.bfloat16), approximate="tanh")
+    x16, rs = _lib.rows_to_f16(hg)
+    y32 = _lib.w4a16_gemm(x16, w2q, w2s, b2.float(), out_dtype=torch.float32, row_scale=rs)
+    ref2 = hg.float() @ dequant_fp32(w2q, w2s).t() + b2.float()
+    err2 = ((y32 - ref2).abs().max() / ref2.abs().max()).item()
+    del ref1, ref2, h32, y32, hg, x16, rs, x16a, rsa
+
+    # ---- timing ---------------------------------------------------------------------------------
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(record=True)
+    torch.cuda.synchronize()
+    elapsed = time.perf_counter() - t0
+    ms_step = elapsed * 1e3 / args.steps
+    flops_step = 2.0 * M_TOKENS * HIDDEN * MLP * 2
+    value = flops_step / (elapsed / args.steps) / 1e12
+    gemm_ms = [a.elapsed_time(b) for a, b in gemm_events]
+    gemm_avg_ms = sum(gemm_ms) / len(gemm_ms)
+    flops_launch = 2.0 * M_TOKENS * HIDDEN * MLP  # fc1 and fc2 have the same 2*M*N*K
+    achieved = flops_launch / (gemm_avg_ms * 1e-3) / 1e12
+
+    traffic = None
+    tpath = os.path.join(HERE, "profiles", "w4a16_gemm_c2_traffic.json")
+    if os.path.exists(tpath):
+        try:
+            traffic = json.load(open(tpath)).get("bytes_per_launch")
+        except Exception:
+            traffic = None
+
+    out = {
+        "metric": "W4A16 GEMM TFLOP/s + % MFMA peak at M=4608 Flux shapes; DiT step ms",
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "f16",
+        "data": "synthetic (seeded random bf16 activations, random int4 group-32 weights in the reference layout)",
+        "config": {"workload": "C2 Flux DiT MLP pair: W4A16 fc1 3072->12288 + GELU-tanh + W4A16 fc2 12288->3072",
+                   "tokens": M_TOKENS, "hidden": HIDDEN, "mlp": MLP, "group": 32, "activations": "bf16",
+                   "route": "row-scaled fp16 staging + fp16 MFMA, fp32 accumulate", "parallelism": "single GPU"},
+        "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                     "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
+                     "kernel": "w4a16_gemm_kernel (fc1 and fc2 launches, HIP events on the launch stream)",
+                     "avg_launch_ms": round(gemm_avg_ms, 4)},
+        "parity": {"fc1_max_rel_err": err1, "fc2_max_rel_err": err2, "gate": GATE,
+                   "pass": bool(err1 <= GATE and err2 <= GATE)},
+    }
+    if not args.no_cpu_baseline:
+        cb = cpu_baseline(orc_bits(x), w1q.cpu().numpy(), w1s.cpu().numpy(), b1.float().cpu().numpy(),
+                          w2q.cpu().numpy(), w2s.cpu().numpy(), b2.float().cpu().numpy(), args.cpu_repeats)
+        cb.pop("_check", None)
+        out["cpu_baseline"] = cb
+    print(json.dumps(out), flush=True)
+
+
+def dequant_fp32(w_q4, w_scale):
+    """fp32 weights of the packed layout (low nibble first, two's complement) times the group
+    scales, on the weights' device: the reference's dequant (nodes.py:43-52) in fp32."""
+    import torch
+    b = w_q4.view(torch.uint8).to(torch.int16)
+    codes = torch.stack([b & 0xF, b >> 4], dim=-1).reshape(w_q4.shape[0], -1)
+    codes = torch.where(codes > 7, codes - 16, codes).float()
+    return codes * w_scale.float().repeat_interleave(32, dim=1)
+
+
+def orc_bits(x):
+    """bf16 tensor -> numpy uint16 bit patterns."""
+    import torch
+    return x.cpu().contiguous().view(torch.int16).numpy().view("uint16")
+
+
+if __name__ == "__main__":
+    main()

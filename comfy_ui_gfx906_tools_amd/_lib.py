@@ -23,6 +23,8 @@ LIB_PATH = os.path.join(_PKG_DIR, "libqlinear.so")
 QL_F32, QL_F16, QL_BF16, QL_I32 = 0, 1, 2, 3
 _DTYPE_CODE = {torch.float32: QL_F32, torch.float16: QL_F16, torch.bfloat16: QL_BF16, torch.int32: QL_I32}
 
+W4A16_BF16_MFMA = 1  # flags: bf16 activations straight into bf16 MFMA (see include/qlinear.h)
+
 RULE_DIV = 0    # scale = amax / 7        (torch on CPU)
 RULE_RECIP = 1  # scale = amax * fl(1/7)  (torch on GPU; the reference kernel)
 
@@ -38,9 +40,10 @@ _c_vp = ctypes.c_void_p
 SIGNATURES = {
     "qlinear_last_error": (ctypes.c_char_p, []),
     "qlinear_abi_version": (_c_int, []),
-    "qlinear_w4a16_workspace_bytes": (_c_size_t, [_c_i64, _c_i64, _c_i64, _c_int, _c_int]),
-    "qlinear_w4a16_gemm": (_c_int, [_c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,
-                                    _c_int, _c_vp, _c_size_t, _c_vp]),
+    "qlinear_w4a16_workspace_bytes": (_c_size_t, [_c_int, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int]),
+    "qlinear_w4a16_gemm": (_c_int, [_c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64,
+                                    _c_i64, _c_int, _c_int, _c_vp, _c_size_t, _c_vp]),
+    "qlinear_rows_to_f16": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
     "qlinear_w4a16_auto_splits": (_c_int, [_c_i64, _c_i64, _c_i64, _c_int]),
     "qlinear_quantize_int4": (_c_int, [_c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
     "qlinear_quantize_int8_per_token": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
@@ -111,16 +114,38 @@ class _Workspaces:
 _workspaces = _Workspaces()
 
 
+def rows_to_f16(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Exact per-row power-of-two scaling of x [M, K] into fp16: (x16 [M, K], row_scale [M])."""
+    lib = load_library()
+    x = _dev_tensor(x, "x")
+    if x.dtype not in (torch.float32, torch.float16, torch.bfloat16) or x.dim() != 2:
+        raise RuntimeError(f"x must be a float32/float16/bfloat16 [M, K] tensor, got {x.dtype} {tuple(x.shape)}")
+    M, K = x.shape
+    x16 = torch.empty((M, K), dtype=torch.float16, device=x.device)
+    rs = torch.empty((M,), dtype=torch.float32, device=x.device)
+    if M == 0:
+        return x16, rs
+    with torch.cuda.device(x.device):
+        rc = lib.qlinear_rows_to_f16(_DTYPE_CODE[x.dtype], x.data_ptr(), x16.data_ptr(), rs.data_ptr(), M, K,
+                                     _stream_ptr(x.device))
+    _check(rc, "rows_to_f16")
+    return x16, rs
+
+
 def w4a16_gemm(x: torch.Tensor, w_q4: torch.Tensor, w_scale: torch.Tensor, bias: torch.Tensor | None = None,
-               out_dtype: torch.dtype | None = None, splits: int = 0) -> torch.Tensor:
+               out_dtype: torch.dtype | None = None, splits: int = 0, bf16_mfma: bool = False,
+               row_scale: torch.Tensor | None = None) -> torch.Tensor:
     """y[M, N] = x[M, K] @ dequant(w_q4, w_scale)^T (+ bias) on the gfx950 W4A16 kernel.
-    x: bf16/fp16 [M, K]; w_q4: int8 [N, K/2]; w_scale: fp32 [N, K/32]; bias: out_dtype [N]."""
+    x: fp16/bf16/fp32 [M, K]; w_q4: int8 [N, K/2]; w_scale: fp32 [N, K/32]; bias: out_dtype [N].
+    bf16 and fp32 activations go through the exact row-scaled fp16 staging unless bf16_mfma is
+    set (then bf16 x meets bf16-rounded weights, the reference's bf16 dequant numerics).
+    row_scale (fp16 x only): per-row factor from rows_to_f16, applied in the epilogue."""
     lib = load_library()
     x = _dev_tensor(x, "x")
     w_q4 = _dev_tensor(w_q4, "w_q4")
     w_scale = _dev_tensor(w_scale, "w_scale")
-    if x.dtype not in (torch.bfloat16, torch.float16):
-        raise RuntimeError(f"x dtype {x.dtype} unsupported, expected bfloat16 or float16")
+    if x.dtype not in (torch.bfloat16, torch.float16, torch.float32):
+        raise RuntimeError(f"x dtype {x.dtype} unsupported, expected bfloat16, float16 or float32")
     if w_q4.dtype not in (torch.int8, torch.uint8) or w_scale.dtype != torch.float32:
         raise RuntimeError(f"w_q4 must be int8 and w_scale float32, got {w_q4.dtype} / {w_scale.dtype}")
     if x.dim() != 2 or w_q4.dim() != 2:
@@ -142,13 +167,22 @@ def w4a16_gemm(x: torch.Tensor, w_q4: torch.Tensor, w_scale: torch.Tensor, bias:
     y = torch.empty((M, N), dtype=out_dtype, device=x.device)
     if M == 0:
         return y
+    flags = W4A16_BF16_MFMA if bf16_mfma else 0
+    xdt = _DTYPE_CODE[x.dtype]
+    if row_scale is not None:
+        row_scale = _dev_tensor(row_scale, "row_scale")
+        if x.dtype != torch.float16 or row_scale.dtype != torch.float32 or row_scale.numel() != M:
+            raise RuntimeError(f"row_scale needs float16 x and a float32 [{M}] tensor, got x {x.dtype}, "
+                               f"row_scale {row_scale.dtype} {tuple(row_scale.shape)}")
     with torch.cuda.device(x.device):
         stream = _stream_ptr(x.device)
-        nbytes = lib.qlinear_w4a16_workspace_bytes(M, N, K, splits, x.device.index)
+        nbytes = lib.qlinear_w4a16_workspace_bytes(xdt, M, N, K, splits, flags, x.device.index)
         ws = _workspaces.get(x.device, stream, nbytes) if nbytes else None
-        rc = lib.qlinear_w4a16_gemm(_DTYPE_CODE[x.dtype], _DTYPE_CODE[out_dtype], x.data_ptr(), w_q4.data_ptr(),
-                                    w_scale.data_ptr(), bias.data_ptr() if bias is not None else None, y.data_ptr(),
-                                    M, N, K, splits, ws.data_ptr() if ws is not None else None,
+        rc = lib.qlinear_w4a16_gemm(xdt, _DTYPE_CODE[out_dtype], x.data_ptr(),
+                                    row_scale.data_ptr() if row_scale is not None else None,
+                                    w_q4.data_ptr(), w_scale.data_ptr(),
+                                    bias.data_ptr() if bias is not None else None, y.data_ptr(), M, N, K, splits,
+                                    flags, ws.data_ptr() if ws is not None else None,
                                     ws.numel() if ws is not None else 0, stream)
     _check(rc, "w4a16_gemm")
     return y

@@ -47,10 +47,10 @@ def hipcc_path() -> str:
     raise RuntimeError("hipcc not found (set HIPCC or install ROCm under /opt/rocm)")
 
 
-def _compile(hipcc: str, src: str, verbose: bool) -> str:
-    obj = os.path.join(BUILD_DIR, os.path.basename(src) + ".o")
-    lang = ["-x", "hip"] if src.endswith(".hip") else ["-x", "hip"]
-    cmd = [hipcc, *COMMON_FLAGS, *lang, "-c", os.path.join(CSRC, src), "-o", obj]
+def _compile(hipcc: str, src: str, verbose: bool, csrc: str = CSRC, build_dir: str = BUILD_DIR,
+             extra: tuple = ()) -> str:
+    obj = os.path.join(build_dir, os.path.basename(src) + ".o")
+    cmd = [hipcc, *COMMON_FLAGS, *extra, "-x", "hip", "-c", os.path.join(csrc, src), "-o", obj]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
@@ -64,30 +64,36 @@ def _compile(hipcc: str, src: str, verbose: bool) -> str:
     return obj
 
 
-def build(jobs: int | None = None, verbose: bool = False) -> str:
-    """Compile every source for gfx950 and link libqlinear.so next to this file."""
+def build(jobs: int | None = None, verbose: bool = False, csrc: str = CSRC, out: str = LIB_PATH,
+          extra_flags: tuple = ()) -> str:
+    """Compile every source for gfx950 and link libqlinear.so next to this file (or `out`, from
+    the sources in `csrc`, with `extra_flags` added)."""
     hipcc = hipcc_path()
-    os.makedirs(BUILD_DIR, exist_ok=True)
+    build_dir = BUILD_DIR if out == LIB_PATH else out + ".build"
+    os.makedirs(build_dir, exist_ok=True)
     jobs = jobs or min(len(SOURCES), os.cpu_count() or 1, 16)
     with ThreadPoolExecutor(max_workers=jobs) as ex:
-        objs = list(ex.map(lambda s: _compile(hipcc, s, verbose), SOURCES))
-    tmp = LIB_PATH + ".tmp"
+        objs = list(ex.map(lambda s: _compile(hipcc, s, verbose, csrc, build_dir, tuple(extra_flags)), SOURCES))
+    tmp = out + ".tmp"
     cmd = [hipcc, "-shared", "-fPIC", f"--offload-arch={ARCH}", *objs, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stdout}\n{res.stderr}")
-    os.replace(tmp, LIB_PATH)
-    return LIB_PATH
+    os.replace(tmp, out)
+    return out
 
 
 def main() -> None:
     ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
     ap.add_argument("--jobs", type=int, default=None)
     ap.add_argument("--verbose", action="store_true")
+    ap.add_argument("--csrc", default=CSRC, help="source directory (default: the package's csrc/)")
+    ap.add_argument("--out", default=LIB_PATH, help="output library path")
+    ap.add_argument("-D", dest="defines", action="append", default=[], help="extra preprocessor define")
     args = ap.parse_args()
-    print(build(args.jobs, args.verbose))
+    print(build(args.jobs, args.verbose, args.csrc, args.out, tuple("-D" + d for d in args.defines)))
 
 
 if __name__ == "__main__":

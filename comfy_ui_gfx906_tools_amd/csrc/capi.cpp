@@ -70,22 +70,33 @@ int device_cus(int device, int* cus) {
 // Tiles first go one per workgroup ("data-parallel"); when that leaves the last wave of a
 // 1-workgroup-per-CU grid badly filled, the tiles of that last wave are cut into ksplit K
 // pieces instead, chosen to minimise the modelled makespan (in tile-times).
-constexpr int kMaxCutTiles = QL_W4A16_COUNTER_BYTES / 4;  // one uint32 counter per cut tile
+// Workspace layout: [row scales: M fp32][x16: M x K fp16][partial tiles: fp32]
+constexpr int kMaxCutTiles = 1 << 16;
 
 struct W4A16Plan {
   int cfg, BM, BN, tiles_m, tiles_n, stages, dp_tiles, ksplit, grid;
-  size_t counter_bytes, partial_bytes;
+  bool prepass;  // stage x as row-scaled fp16
+  size_t off_row_scale, off_x16, off_partial, total;
 };
 
-// Config 0 (256 x 256) is built but not selected: its cut-tile path still spills registers.
+size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
+
+// Tile height for large M: 128 rows (config 1) or 256 rows (config 0). 128 measures faster:
+// at 256 rows the 256 accumulators leave the compiler no registers to pipeline operand reads.
+#ifndef QL_W4A16_LARGE_CFG
+#define QL_W4A16_LARGE_CFG 1
+#endif
+
 int w4a16_cfg_for(int64_t M) {
   if (M <= 16) return 3;
   if (M <= 64) return 2;
-  return 1;
+  if (M <= 128) return 1;
+  return QL_W4A16_LARGE_CFG;
 }
 
-W4A16Plan plan_w4a16(int64_t M, int64_t N, int64_t K, int splits, int cus) {
+W4A16Plan plan_w4a16(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, int flags, int cus) {
   W4A16Plan pl{};
+  pl.prepass = x_dtype == QL_F32 || (x_dtype == QL_BF16 && !(flags & QL_W4A16_BF16_MFMA));
   pl.cfg = w4a16_cfg_for(M);
   const W4A16Config& c = w4a16_config(pl.cfg);
   pl.BM = c.BM;
@@ -121,14 +132,13 @@ W4A16Plan plan_w4a16(int64_t M, int64_t N, int64_t K, int splits, int cus) {
     }
   }
   pl.grid = pl.dp_tiles + (tiles - pl.dp_tiles) * pl.ksplit;
-  pl.counter_bytes = QL_W4A16_COUNTER_BYTES;
-  pl.partial_bytes =
+  const size_t partial_bytes =
       pl.dp_tiles < tiles ? (size_t)(tiles - pl.dp_tiles) * pl.ksplit * pl.BM * pl.BN * sizeof(float) : 0;
+  pl.off_row_scale = 0;
+  pl.off_x16 = pl.off_row_scale + (pl.prepass ? align256((size_t)M * sizeof(float)) : 0);
+  pl.off_partial = pl.off_x16 + (pl.prepass ? align256((size_t)M * K * 2) : 0);
+  pl.total = (pl.prepass || partial_bytes) ? pl.off_partial + partial_bytes : 0;
   return pl;
-}
-
-size_t w4a16_ws_bytes(const W4A16Plan& pl) {
-  return pl.partial_bytes ? pl.counter_bytes + pl.partial_bytes : 0;
 }
 
 int check_w4a16_shape(int64_t M, int64_t N, int64_t K) {
@@ -148,11 +158,12 @@ const char* qlinear_last_error(void) { return g_last_error.c_str(); }
 
 int qlinear_abi_version(void) { return (1 << 16) | 0; }
 
-size_t qlinear_w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int splits, int device) {
+size_t qlinear_w4a16_workspace_bytes(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, int flags,
+                                     int device) {
   if (check_w4a16_shape(M, N, K) != QL_OK || M == 0) return 0;
   int cus = 0;
   if (device_cus(device, &cus) != QL_OK) return 0;
-  return w4a16_ws_bytes(plan_w4a16(M, N, K, splits, cus));
+  return plan_w4a16(x_dtype, M, N, K, splits, flags, cus).total;
 }
 
 int qlinear_w4a16_auto_splits(int64_t M, int64_t N, int64_t K, int device) {
@@ -160,41 +171,54 @@ int qlinear_w4a16_auto_splits(int64_t M, int64_t N, int64_t K, int device) {
   int cus = 0;
   if (int rc = device_cus(device, &cus)) return -rc;
   if (M == 0) return 1;
-  const W4A16Plan pl = plan_w4a16(M, N, K, 0, cus);
+  const W4A16Plan pl = plan_w4a16(QL_F16, M, N, K, 0, 0, cus);
   return pl.dp_tiles < pl.tiles_m * pl.tiles_n ? pl.ksplit : 1;
 }
 
-int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const void* w_q4, const float* w_scale,
-                       const void* bias, void* y, int64_t M, int64_t N, int64_t K, int splits, void* workspace,
-                       size_t workspace_bytes, void* stream) {
-  if (x_dtype != QL_BF16 && x_dtype != QL_F16)
-    return fail(QL_ERR_DTYPE, "x dtype %s (%d) unsupported, expected bfloat16 or float16", dtype_name(x_dtype), x_dtype);
+int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const float* row_scale, const void* w_q4,
+                       const float* w_scale, const void* bias, void* y, int64_t M, int64_t N, int64_t K, int splits,
+                       int flags, void* workspace, size_t workspace_bytes, void* stream) {
+  if (x_dtype != QL_BF16 && x_dtype != QL_F16 && x_dtype != QL_F32)
+    return fail(QL_ERR_DTYPE, "x dtype %s (%d) unsupported, expected bfloat16, float16 or float32", dtype_name(x_dtype),
+                x_dtype);
   if (out_dtype != QL_F32 && out_dtype != QL_F16 && out_dtype != QL_BF16)
     return fail(QL_ERR_DTYPE, "out dtype %s (%d) unsupported, expected float32/float16/bfloat16", dtype_name(out_dtype),
                 out_dtype);
   if (int rc = check_w4a16_shape(M, N, K)) return rc;
   if (splits < 0 || splits > 64) return fail(QL_ERR_ARG, "splits must be in [0, 64], got %d", splits);
+  if (flags & ~QL_W4A16_BF16_MFMA) return fail(QL_ERR_ARG, "unknown flags 0x%x", flags);
+  if (row_scale && x_dtype != QL_F16)
+    return fail(QL_ERR_ARG, "row_scale is only accepted with float16 x (from qlinear_rows_to_f16), got %s",
+                dtype_name(x_dtype));
   if (M == 0) return ok();
   if (!x || !w_q4 || !w_scale || !y) return fail(QL_ERR_ARG, "null x / w_q4 / w_scale / y pointer");
   if (!aligned16(x) || !aligned16(w_q4))
     return fail(QL_ERR_ALIGN, "x and w_q4 must be 16-byte aligned (x=%p w_q4=%p)", x, w_q4);
   int cus = 0;
   if (int rc = device_cus(-1, &cus)) return rc;
-  const W4A16Plan pl = plan_w4a16(M, N, K, splits, cus);
-  const size_t need = w4a16_ws_bytes(pl);
-  if (need > 0 && (!workspace || workspace_bytes < need))
-    return fail(QL_ERR_WORKSPACE, "workspace of %zu bytes needed (M=%lld N=%lld K=%lld splits=%d), got %zu at %p", need,
-                (long long)M, (long long)N, (long long)K, splits, workspace_bytes, workspace);
-  if (need > 0 && !aligned16(workspace)) return fail(QL_ERR_ALIGN, "workspace must be 16-byte aligned");
+  const W4A16Plan pl = plan_w4a16(x_dtype, M, N, K, splits, flags, cus);
+  if (pl.total > 0 && (!workspace || workspace_bytes < pl.total))
+    return fail(QL_ERR_WORKSPACE, "workspace of %zu bytes needed (M=%lld N=%lld K=%lld splits=%d flags=%d), got %zu at %p",
+                pl.total, (long long)M, (long long)N, (long long)K, splits, flags, workspace_bytes, workspace);
+  if (pl.total > 0 && !aligned16(workspace)) return fail(QL_ERR_ALIGN, "workspace must be 16-byte aligned");
 
+  char* ws = (char*)workspace;
   W4A16Params p{};
   p.x = x;
+  p.row_scale = row_scale;
+  if (pl.prepass) {
+    float* rs = (float*)(ws + pl.off_row_scale);
+    void* x16 = ws + pl.off_x16;
+    const hipError_t e = rows_to_scaled_f16_launch(x_dtype, x, x16, rs, M, K, (hipStream_t)stream);
+    if (e != hipSuccess) return fail(QL_ERR_LAUNCH, "fp16 staging launch failed: %s", hipGetErrorString(e));
+    p.x = x16;
+    p.row_scale = rs;
+  }
   p.wq = w_q4;
   p.ws = w_scale;
   p.bias = bias;
   p.y = y;
-  p.counters = need ? (uint32_t*)workspace : nullptr;
-  p.partial = need ? (float*)((char*)workspace + pl.counter_bytes) : nullptr;
+  p.partial = pl.total ? (float*)(ws + pl.off_partial) : nullptr;
   p.M = (int)M;
   p.N = (int)N;
   p.K = (int)K;
@@ -204,8 +228,24 @@ int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const void* w_
   p.stages = pl.stages;
   p.dp_tiles = pl.dp_tiles;
   p.ksplit = pl.ksplit;
-  const hipError_t e = w4a16_launch(pl.cfg, x_dtype == QL_BF16, p, pl.grid, (hipStream_t)stream);
+  const bool bf16_mfma = x_dtype == QL_BF16 && !pl.prepass;
+  const hipError_t e = w4a16_launch(pl.cfg, bf16_mfma, p, (hipStream_t)stream);
   if (e != hipSuccess) return fail(QL_ERR_LAUNCH, "w4a16 launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int qlinear_rows_to_f16(int x_dtype, const void* x, void* x16, float* row_scale, int64_t M, int64_t K,
+                        void* stream) {
+  if (x_dtype != QL_F32 && x_dtype != QL_F16 && x_dtype != QL_BF16)
+    return fail(QL_ERR_DTYPE, "unsupported dtype %s (%d), expected float32/float16/bfloat16", dtype_name(x_dtype),
+                x_dtype);
+  if (M < 0 || K <= 0 || K % 8 != 0 || K > INT32_MAX / 2 || M > INT32_MAX)
+    return fail(QL_ERR_SHAPE, "x must be [M, K] with K %% 8 == 0, got [%lld, %lld]", (long long)M, (long long)K);
+  if (M == 0) return ok();
+  if (!x || !x16 || !row_scale) return fail(QL_ERR_ARG, "null x / x16 / row_scale pointer");
+  if (!aligned16(x) || !aligned16(x16)) return fail(QL_ERR_ALIGN, "x and x16 must be 16-byte aligned");
+  const hipError_t e = rows_to_scaled_f16_launch(x_dtype, x, x16, row_scale, M, K, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(QL_ERR_LAUNCH, "rows_to_f16 launch failed: %s", hipGetErrorString(e));
   return ok();
 }
 

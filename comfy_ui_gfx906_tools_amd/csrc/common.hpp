@@ -103,7 +103,11 @@ __device__ __forceinline__ i32x4 mfma16_i8(u32x4 a, u32x4 b, i32x4 c) {
 __device__ __forceinline__ void load_lds16(const void* gptr, void* lds_base) {
   __builtin_amdgcn_global_load_lds(gptr, (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
 }
-__device__ __forceinline__ void wait_vmem() { asm volatile("s_waitcnt vmcnt(0)" ::: "memory"); }
+// s_waitcnt as a real instruction (not inline asm), so the compiler's own wait insertion knows
+// which counters are already drained. gfx9 encoding: vmcnt [3:0]+[15:14], expcnt [6:4],
+// lgkmcnt [11:8]; a field at its maximum means "do not wait" on that counter.
+__device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }   // vmcnt(0)
+__device__ __forceinline__ void wait_lgkm() { __builtin_amdgcn_s_waitcnt(0xC07F); }   // lgkmcnt(0)
 
 // ---- workgroup -> tile order ---------------------------------------------------------------
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2). Renumber them

@@ -13,8 +13,8 @@ struct W4A16Params {
   const float* ws;       // [N, K/32]
   const void* bias;      // [N] out dtype, or null
   void* y;               // [M, N] out dtype
-  float* partial;        // partial tiles: (tiles - dp_tiles) * ksplit slots of BM * BN fp32
-  uint32_t* counters;    // one per cut tile (tile - dp_tiles), zero between calls
+  const float* row_scale;  // [M] power-of-two factor applied in the epilogue, or null
+  float* partial;        // partial tiles of the cut tiles: (tiles - dp_tiles) * ksplit slots of BM * BN fp32
   int M, N, K;
   int out_dtype;
   int tiles_m, tiles_n;
@@ -28,7 +28,9 @@ struct W4A16Config {
 };
 
 const W4A16Config& w4a16_config(int id);
-hipError_t w4a16_launch(int cfg, bool bf16, const W4A16Params& p, int grid, hipStream_t stream);
+hipError_t w4a16_launch(int cfg, bool bf16, const W4A16Params& p, hipStream_t stream);
+hipError_t rows_to_scaled_f16_launch(int dtype, const void* x, void* x16, float* row_scale, int64_t M,
+                                     int64_t K, hipStream_t stream);
 
 struct W8A8Params {
   const int8_t* xq;      // [M, K]

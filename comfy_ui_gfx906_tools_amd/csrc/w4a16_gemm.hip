@@ -1,30 +1,32 @@
-// W4A16 GEMM for gfx950: y[M,N] = x[M,K] @ (q[N,K] * s[N,K/32])^T (+ bias), x bf16/fp16,
+// W4A16 GEMM for gfx950: y[M,N] = x[M,K] @ (q[N,K] * s[N,K/32])^T (+ bias), x fp16/bf16,
 // q packed int4 in the reference layout (nodes/ComfyUI-Gfx906Int4/ops.py:108-126), fp32 group
 // scales, fp32 MFMA accumulation.
 //
 // The reference computes this product as dequantize-then-matmul (nodes.py:43-52, 116) and its
 // production kernel is a W4A4 v_dot8 GEMM (csrc/int4_gemm_scaled.hip:53-180); neither is the
-// shape of this kernel. Design, per workgroup of NWM x NWN waves and a BM x BN output tile:
+// shape of this kernel. Design, per 256-thread workgroup (4 waves side by side along N) and a
+// BM x BN output tile:
 //
 // * A (activations) is staged HBM -> LDS with global_load_lds_dwordx4, 128 K per stage, double
-//   buffered. A row of a stage is 256 B = 16 chunks of 16 B; chunk c of row r sits at
-//   slot c ^ (r & 15), so the 16 rows an MFMA operand read touches hit 16 distinct bank groups.
-//   Rows past M are clamped to row M-1 (their outputs are never stored); K past the end is
-//   clamped to the last chunk and meets zero weights.
-// * B (weights) never touches LDS. Lane (c = l%16, j = l/16) of a wave loads 16 B of weight
-//   row n = col0 + c: the whole 32-element quant group j of the stage, with its one scale, and
-//   dequantizes it in registers (dequant8: int4 -> q*s -> bf16/fp16). The MFMA K-slot map is
-//   permuted to match: MFMA i of a stage takes, in K-slot block j, elements 32j + 8i .. +7.
-//   A is read from LDS with the same map (chunk 4j + i), so every lane's load is one group.
-// * Each wave owns a 16*WM x 16*WN sub-tile: WM*WN accumulators of 16x16, v_mfma_f32_16x16x32.
-//   With WM = 16 a wave's dequant work is 0.5 element per MFMA, which hides under the MFMA.
-// * Scheduling: every workgroup runs exactly one K range of one tile. The first dp_tiles tiles
-//   are whole (one workgroup each); each remaining tile is cut into ksplit K ranges, so a grid
-//   that would leave CUs idle in its last wave is evened out. A cut tile is finished by the
-//   workgroup that arrives last on its counter: it sums the fp32 partials of all pieces in
-//   piece order (deterministic), adds the bias and stores. No workgroup ever waits on another.
-//   (One segment per workgroup keeps the accumulators' live range simple enough for the
-//   register allocator to leave them in AGPRs.)
+//   buffered in two distinct arrays. A row of a stage is 256 B = 16 chunks of 16 B; chunk c of
+//   row r sits at slot c ^ (r & 15), so the 16 rows an MFMA operand read touches hit 16
+//   distinct bank groups. Rows past M are clamped to row M-1 (their outputs are never stored);
+//   K past the end is clamped to the last chunk and meets zero weights.
+// * B (weights) never touches LDS. Lane (c = l%16, j = l/16) of a wave loads 16 B of weight row
+//   n = col0 + c: the whole 32-element quant group j of the stage, with its one scale, and
+//   dequantizes it in registers (dequant8: int4 -> q*s -> fp16/bf16). The MFMA K-slot map is
+//   permuted to match: MFMA i of a stage takes, in K-slot block j, elements 32j + 8i .. +7; A is
+//   read from LDS with the same map (chunk 4j + i), so every lane's load is one group.
+// * Each wave owns a (16*WM) x (16*WN) sub-tile of 16x16 accumulators (v_mfma_f32_16x16x32).
+//   With WM = 16 the dequant costs 0.5 element per MFMA.
+// * Optional row scales (the fp16 route for bf16 activations): x arrives pre-scaled per row by
+//   2^-e (exact) and the epilogue multiplies by 2^e (exact).
+// * Scheduling: every workgroup runs one K range of one tile. The first dp_tiles tiles are
+//   whole (kernel instance kCut = false); each remaining tile is cut into ksplit K ranges
+//   (kCut = true, launched next on the same stream) whose fp32 partials a third kernel sums in
+//   piece order (deterministic), with bias and row scale. Stream order makes the partials
+//   visible to the reduction -- no fences or counters inside the GEMM, which on MI355X's
+//   per-XCD L2s would force L2 write-backs.
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -32,234 +34,349 @@ namespace qlinear {
 
 namespace {
 
-constexpr int kStageK = 128;          // K per pipeline stage (16-bit elements); S counts
-                                      // steps of two stages
-constexpr int kRowBytes = 256;        // one A row of a stage
-constexpr int kGroupsPerStage = 4;    // 128 / 32
+constexpr int kStageK = 128;        // K per pipeline stage (16-bit elements)
+constexpr int kRowBytes = 256;      // one A row of a stage
+constexpr int kGroupsPerStage = 4;  // 128 / 32
 constexpr int kGroupM = 8;
+constexpr int kWaves = 4;
 
-template <bool kBf16, int WM, int WN, int NWM, int NWN>
-__global__ __launch_bounds__(64 * NWM * NWN) void w4a16_gemm_kernel(W4A16Params p) {
-  constexpr int NW = NWM * NWN;
-  constexpr int BM = 16 * WM * NWM;
-  constexpr int BN = 16 * WN * NWN;
+template <bool kBf16, int WM, int WN, bool kCut, bool kRegA>
+__global__ __launch_bounds__(64 * kWaves) void w4a16_gemm_kernel(W4A16Params p) {
+  constexpr int BM = 16 * WM;
+  constexpr int BN = 16 * WN * kWaves;
   constexpr int kStageBytes = BM * kRowBytes;
-  constexpr int kBlocksPerWave = BM / 4 / NW;  // 1024-B LDS blocks each wave fills per stage
-  static_assert(BM % (4 * NW) == 0, "A tile must split into whole 1 KiB blocks per wave");
+  constexpr int kBlocksPerWave = BM / 4 / kWaves;  // 1 KiB LDS blocks each wave fills per stage
+  static_assert(BM % (4 * kWaves) == 0, "A tile must split into whole 1 KiB blocks per wave");
   // Two distinct arrays (not one indexed by stage parity): the compiler's alias analysis then
-  // sees that operand reads of one buffer never touch the DMA target of the other, and does
-  // not wait for the next stage's loads before the current stage's MFMAs.
+  // sees that operand reads of one buffer never touch the DMA target of the other, and does not
+  // wait for the next stage's loads before the current stage's MFMAs.
   __shared__ __attribute__((aligned(1024))) uint8_t lds0[kStageBytes];
   __shared__ __attribute__((aligned(1024))) uint8_t lds1[kStageBytes];
-  __shared__ int s_last;
 
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int wm = wave / NWN, wn = wave % NWN;
+  const int wn = threadIdx.x >> 6;
   const int r16 = lane & 15, j4 = lane >> 4;
   const int M = p.M, N = p.N, K = p.K;
   const int groups = K / kGroup;
-  const size_t wrow = (size_t)K / 2;
-  const int S = p.stages;
+  const int S = p.stages;  // steps of two stages
 
   const uint16_t* __restrict__ x = (const uint16_t*)p.x;
-  const uint8_t* __restrict__ wq = (const uint8_t*)p.wq;
-  const float* __restrict__ ws = p.ws;
-
-  const int g = xcd_remap(blockIdx.x, gridDim.x);
-
-  f32x4 acc[WM][WN];
-
-  // ---- one K-stage range [s0, s1) of tile t --------------------------------------------
-  auto run_segment = [&](int t, int s0, int s1, int& m0, int& n0) {
-    int tm, tn;
-    tile_coords(t, p.tiles_m, p.tiles_n, kGroupM, tm, tn);
-    m0 = tm * BM;
-    n0 = tn * BN;
-
-    const uint8_t* bptr[WN];
-    const float* sptr[WN];
-    bool bok[WN];
-#pragma unroll
-    for (int fn = 0; fn < WN; ++fn) {
-      const int n = n0 + (wn * WN + fn) * 16 + r16;
-      bok[fn] = n < N;
-      const int nc = min(n, N - 1);
-      bptr[fn] = wq + (size_t)nc * wrow;
-      sptr[fn] = ws + (size_t)nc * groups;
-    }
-
-    auto issue_a = [&](int s, uint8_t* buf) {
-#pragma unroll
-      for (int q = 0; q < kBlocksPerWave; ++q) {
-        const int blk = wave * kBlocksPerWave + q;
-        const int row = blk * 4 + j4;
-        const int lch = r16 ^ (row & 15);
-        const int gm = min(m0 + row, M - 1);
-        const int gk = min(s * kStageK + lch * 8, K - 8);
-        load_lds16(x + (size_t)gm * K + gk, buf + blk * 1024);
-      }
-    };
-    // Raw loads only; the zero-scale select for columns past N / groups past K is applied by
-    // the stage that consumes them, so no wait is forced right after the loads are issued.
-    auto load_b = [&](int s, u32x4 (&raw)[WN], float (&sc)[WN]) {
-      const int kgc = min(s * kGroupsPerStage + j4, groups - 1);
-#pragma unroll
-      for (int fn = 0; fn < WN; ++fn) {
-        raw[fn] = *(const u32x4*)(bptr[fn] + (size_t)kgc * 16);
-        sc[fn] = sptr[fn][kgc];
-      }
-    };
-
-#pragma unroll
-    for (int fm = 0; fm < WM; ++fm)
-#pragma unroll
-      for (int fn = 0; fn < WN; ++fn) acc[fm][fn] = f32x4{0.f, 0.f, 0.f, 0.f};
-
-    u32x4 rawn[WN];
-    float scn[WN];
-    // one pipeline stage: operands of stage s are in `cur`; stage s+1 is fetched into `nxt`
-    auto stage = [&](int s, int k_end, const uint8_t* cur, uint8_t* nxt) {
-      wait_vmem();
-      __syncthreads();
-      u32x4 raw[WN];
-      float sc[WN], neg8s[WN];
-      const bool kok = s * kGroupsPerStage + j4 < groups;
-#pragma unroll
-      for (int fn = 0; fn < WN; ++fn) {
-        raw[fn] = rawn[fn];
-        sc[fn] = (bok[fn] && kok) ? scn[fn] : 0.0f;  // zero scale -> exact zero weights
-        neg8s[fn] = -8.0f * sc[fn];
-      }
-      if (s + 1 < k_end) {
-        issue_a(s + 1, nxt);
-        load_b(s + 1, rawn, scn);
-      }
-      const uint8_t* abase = cur + (wm * WM * 16 + r16) * kRowBytes;
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        u32x4 b[WN];
-#pragma unroll
-        for (int fn = 0; fn < WN; ++fn) b[fn] = dequant8<kBf16>(raw[fn][i], sc[fn], neg8s[fn]);
-        const int pch = (4 * j4 + i) ^ r16;
-#pragma unroll
-        for (int fm = 0; fm < WM; ++fm) {
-          const u32x4 a = *(const u32x4*)(abase + fm * 16 * kRowBytes + pch * 16);
-#pragma unroll
-          for (int fn = 0; fn < WN; ++fn) acc[fm][fn] = mfma16<kBf16>(a, b[fn], acc[fm][fn]);
-        }
-        // keep each K-step's operand reads and dequant inside the step: bounds live registers
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    };
-    // Segments are counted in steps of two stages (256 K), so both halves of the unrolled
-    // loop body run unconditionally and the accumulators stay in one register class.
-    const int k_end = 2 * s1;  // first stage not in this segment
-    issue_a(2 * s0, lds0);
-    load_b(2 * s0, rawn, scn);
-    for (int sp = s0; sp < s1; ++sp) {
-      stage(2 * sp, k_end, lds0, lds1);
-      stage(2 * sp + 1, k_end, lds1, lds0);
-    }
-    __syncthreads();  // the next segment refills both LDS buffers
-  };
-
-  // ---- epilogues -----------------------------------------------------------------------
-  auto store_tile = [&](int m0, int n0) {
-#pragma unroll
-    for (int fn = 0; fn < WN; ++fn) {
-      const int n = n0 + (wn * WN + fn) * 16 + r16;
-      if (n >= N) continue;
-      const float bv = p.bias ? read_elem(p.bias, p.out_dtype, n) : 0.0f;
-#pragma unroll
-      for (int fm = 0; fm < WM; ++fm) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int m = m0 + (wm * WM + fm) * 16 + 4 * j4 + e;
-          if (m < M) write_elem(p.y, p.out_dtype, (size_t)m * N + n, __fadd_rn(acc[fm][fn][e], bv));
-        }
-      }
-    }
-  };
-  auto partial_index = [&](int fm, int fn, int e) {
-    const int lm = (wm * WM + fm) * 16 + 4 * j4 + e;
-    const int ln = (wn * WN + fn) * 16 + r16;
-    return lm * BN + ln;
-  };
 
   // ---- this workgroup's segment ----------------------------------------------------------
-  int t, s0, s1, piece = 0;
-  if (g < p.dp_tiles) {
+  const int g = xcd_remap(blockIdx.x, gridDim.x);
+  int t, s0, s1;
+  if constexpr (!kCut) {
     t = g;
     s0 = 0;
     s1 = S;
   } else {
-    const int r = g - p.dp_tiles;
-    t = p.dp_tiles + r / p.ksplit;
-    piece = r - (t - p.dp_tiles) * p.ksplit;
+    t = p.dp_tiles + g / p.ksplit;
+    const int piece = g - (t - p.dp_tiles) * p.ksplit;
     s0 = (int)((long long)piece * S / p.ksplit);
     s1 = (int)((long long)(piece + 1) * S / p.ksplit);
   }
-  int m0, n0;
-  run_segment(t, s0, s1, m0, n0);
-  if (g < p.dp_tiles) {
-    store_tile(m0, n0);
-    return;
+  int tm, tn;
+  tile_coords(t, p.tiles_m, p.tiles_n, kGroupM, tm, tn);
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  // ---- B addressing ------------------------------------------------------------------------
+  const uint8_t* bptr[WN];
+  const float* sptr[WN];
+  bool bok[WN];
+#pragma unroll
+  for (int fn = 0; fn < WN; ++fn) {
+    const int n = n0 + (wn * WN + fn) * 16 + r16;
+    bok[fn] = n < N;
+    const int nc = min(n, N - 1);
+    bptr[fn] = (const uint8_t*)p.wq + (size_t)nc * (K / 2);
+    sptr[fn] = p.ws + (size_t)nc * groups;
   }
 
-  // ---- cut tile: publish this piece, the last arriving piece finishes the tile ------------
-  const size_t tile_elems = (size_t)BM * BN;
-  float* part = p.partial + (size_t)(g - p.dp_tiles) * tile_elems;  // slot = (tile, piece)
+  // A staging, either HBM -> LDS directly (global_load_lds_dwordx4) or through registers
+  // (global_load_dwordx4, then ds_write_b128 at the end of the stage). Same LDS layout.
+  u32x4 areg[kRegA ? kBlocksPerWave : 1];
+  auto a_src = [&](int s, int q) {
+    const int blk = wn * kBlocksPerWave + q;
+    const int row = blk * 4 + j4;
+    const int lch = r16 ^ (row & 15);
+    const int gm = min(m0 + row, M - 1);
+    const int gk = min(s * kStageK + lch * 8, K - 8);
+    return x + (size_t)gm * K + gk;
+  };
+  auto issue_a = [&](int s, uint8_t* buf) {
+#pragma unroll
+    for (int q = 0; q < kBlocksPerWave; ++q) {
+      if constexpr (kRegA) {
+        areg[q] = *(const u32x4*)a_src(s, q);
+      } else {
+        load_lds16(a_src(s, q), buf + (wn * kBlocksPerWave + q) * 1024);
+      }
+    }
+  };
+  auto commit_a = [&](uint8_t* buf) {
+    if constexpr (kRegA) {
+#pragma unroll
+      for (int q = 0; q < kBlocksPerWave; ++q) *(u32x4*)(buf + (wn * kBlocksPerWave + q) * 1024 + lane * 16) = areg[q];
+    }
+  };
+  // Raw loads only; the zero-scale select for columns past N / groups past K is applied by the
+  // stage that consumes them, so no wait is forced right after the loads are issued.
+  auto load_b = [&](int s, u32x4 (&raw)[WN], float (&sc)[WN]) {
+    const int kgc = min(s * kGroupsPerStage + j4, groups - 1);
+#pragma unroll
+    for (int fn = 0; fn < WN; ++fn) {
+      raw[fn] = *(const u32x4*)(bptr[fn] + (size_t)kgc * 16);
+      sc[fn] = sptr[fn][kgc];
+    }
+  };
+
+  f32x4 acc[WM][WN];
 #pragma unroll
   for (int fm = 0; fm < WM; ++fm)
 #pragma unroll
-    for (int fn = 0; fn < WN; ++fn)
+    for (int fn = 0; fn < WN; ++fn) acc[fm][fn] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  // Two register sets for the raw weights, alternating with the two LDS buffers.
+  u32x4 rawA[WN], rawB[WN];
+  float scA[WN], scB[WN];
+
+  // One pipeline stage: operands of stage s are in `cur` (LDS) and raw/scr (registers); stage s+1
+  // is fetched into `nxt` and raw_n/sc_n. Order matters: the stage's own registers are consumed
+  // (first dequant, first operand reads) before the next loads are issued, so the waits the
+  // compiler places for them never also wait for the next stage's loads.
+  auto stage = [&](int s, int s_end, const uint8_t* cur, uint8_t* nxt, u32x4 (&raw)[WN], float (&scr)[WN],
+                   u32x4 (&raw_n)[WN], float (&sc_n)[WN]) {
+    wait_vmem();
+    __syncthreads();
+    float sc[WN], neg8s[WN];
+    const bool kok = s * kGroupsPerStage + j4 < groups;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) part[partial_index(fm, fn, e)] = acc[fm][fn][e];
-  __threadfence();
-  __syncthreads();
-  if (threadIdx.x == 0) {
-    const unsigned old = atomicAdd(&p.counters[t - p.dp_tiles], 1u);
-    s_last = (old == (unsigned)(p.ksplit - 1));
-  }
-  __syncthreads();
-  if (!s_last) return;
-  __threadfence();
-  const float* first = p.partial + (size_t)(t - p.dp_tiles) * p.ksplit * tile_elems;
-  for (int idx = threadIdx.x * 4; idx < BM * BN; idx += NW * 64 * 4) {
-    f32x4 v = *(const f32x4*)(first + idx);
-    for (int q = 1; q < p.ksplit; ++q) {
-      const f32x4 w = *(const f32x4*)(first + (size_t)q * tile_elems + idx);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) v[e] = __fadd_rn(v[e], w[e]);
+    for (int fn = 0; fn < WN; ++fn) {
+      sc[fn] = (bok[fn] && kok) ? scr[fn] : 0.0f;  // zero scale -> exact zero weights
+      neg8s[fn] = -8.0f * sc[fn];
     }
-    const int m = m0 + idx / BN;
-    if (m >= M) continue;
+    u32x4 b[WN];
+#pragma unroll
+    for (int fn = 0; fn < WN; ++fn) b[fn] = dequant8<kBf16>(raw[fn][0], sc[fn], neg8s[fn]);
+
+    // A operand blocks q = i * WM + fm (K-step i, 16-row block fm); ring of three registers,
+    // reads issued two blocks ahead of their MFMAs
+    const uint8_t* abase = cur + r16 * kRowBytes;
+    auto a_addr = [&](int q) {
+      const int i = q / WM, fm = q % WM;
+      return (const u32x4*)(abase + fm * 16 * kRowBytes + (((4 * j4 + i) ^ r16) * 16));
+    };
+    constexpr int kBlocks = 4 * WM;
+    u32x4 ar[3];
+    ar[0] = *a_addr(0);
+    if (kBlocks > 1) ar[1] = *a_addr(1);
+    __builtin_amdgcn_sched_barrier(0);
+
+    if (s + 1 < s_end) {
+      issue_a(s + 1, nxt);
+      load_b(s + 1, raw_n, sc_n);
+    }
+
+    u32x4 bn[WN];
+#pragma unroll
+    for (int q = 0; q < kBlocks; ++q) {
+      const int i = q / WM, fm = q % WM;
+      if (q + 2 < kBlocks) ar[(q + 2) % 3] = *a_addr(q + 2);
+      if (fm == 0 && i > 0) {
+#pragma unroll
+        for (int fn = 0; fn < WN; ++fn) b[fn] = bn[fn];
+      }
+#pragma unroll
+      for (int fn = 0; fn < WN; ++fn) acc[fm][fn] = mfma16<kBf16>(ar[q % 3], b[fn], acc[fm][fn]);
+      // dequant of K-step i+1, spread over the 16-row blocks: column block fn goes with row
+      // block fn % WM (all of them with the first row block when WM == 1)
+      if (i < 3) {
+#pragma unroll
+        for (int fn = 0; fn < WN; ++fn)
+          if (fn % WM == fm) bn[fn] = dequant8<kBf16>(raw[fn][i + 1], sc[fn], neg8s[fn]);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    if (s + 1 < s_end) commit_a(nxt);
+  };
+
+  // Segments are counted in steps of two stages (256 K), so both halves of the unrolled loop
+  // body run unconditionally and the accumulators stay in one register class.
+  const int s_end = 2 * s1;
+  issue_a(2 * s0, lds0);
+  commit_a(lds0);
+  load_b(2 * s0, rawA, scA);
+  // Drain the kernel-argument scalar loads: with none pending, the compiler can wait for LDS
+  // operand reads with partial lgkmcnt counts instead of lgkmcnt(0).
+  wait_lgkm();
+  for (int sp = s0; sp < s1; ++sp) {
+    stage(2 * sp, s_end, lds0, lds1, rawA, scA, rawB, scB);
+    stage(2 * sp + 1, s_end, lds1, lds0, rawB, scB, rawA, scA);
+  }
+
+  // ---- epilogue ----------------------------------------------------------------------------
+  // A whole tile goes to y (row scale, bias, out dtype); a cut tile's piece goes as plain fp32 to
+  // its partial slot, a tile-local [BM][BN] array. Same store loop for both.
+  void* dst = p.y;
+  int dst_m0 = m0, dst_n0 = n0, dst_M = M, dst_N = N, dst_dtype = p.out_dtype;
+  const void* bias = p.bias;
+  const float* row_scale = p.row_scale;
+  if constexpr (kCut) {
+    dst = p.partial + (size_t)g * (BM * BN);
+    dst_m0 = 0;
+    dst_n0 = 0;
+    dst_M = BM;
+    dst_N = BN;
+    dst_dtype = kF32;
+    bias = nullptr;
+    row_scale = nullptr;
+  }
+  float bv[WN];
+#pragma unroll
+  for (int fn = 0; fn < WN; ++fn) {
+    const int n = dst_n0 + (wn * WN + fn) * 16 + r16;
+    bv[fn] = (bias && n < dst_N) ? read_elem(bias, dst_dtype, n) : 0.0f;
+  }
+  // one 16-row block at a time, fenced, so the row scales and addresses of all rows are never
+  // live together
+#pragma unroll
+  for (int fm = 0; fm < WM; ++fm) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int n = n0 + idx % BN + e;
-      if (n >= N) continue;
-      const float bv = p.bias ? read_elem(p.bias, p.out_dtype, n) : 0.0f;
-      write_elem(p.y, p.out_dtype, (size_t)m * N + n, __fadd_rn(v[e], bv));
+      const int m = dst_m0 + fm * 16 + 4 * j4 + e;
+      if (m >= dst_M) continue;
+      const float rs = row_scale ? row_scale[m] : 1.0f;
+#pragma unroll
+      for (int fn = 0; fn < WN; ++fn) {
+        const int n = dst_n0 + (wn * WN + fn) * 16 + r16;
+        if (n < dst_N) write_elem(dst, dst_dtype, (size_t)m * dst_N + n, acc[fm][fn][e] * rs + bv[fn]);
+      }
     }
+    __builtin_amdgcn_sched_barrier(0);
   }
-  if (threadIdx.x == 0) p.counters[t - p.dp_tiles] = 0u;  // ready for the next call
+}
+
+// Sums the ksplit fp32 partials of every cut tile in piece order, applies the row scale and the
+// bias, and stores y. Grid: (cut tiles) x (BM*BN / 1024) workgroups of 256 threads, 4 elements
+// per thread.
+__global__ __launch_bounds__(256) void w4a16_reduce_kernel(W4A16Params p, int BM, int BN) {
+  const int tl = blockIdx.y;  // cut tile index
+  const int t = p.dp_tiles + tl;
+  int tm, tn;
+  tile_coords(t, p.tiles_m, p.tiles_n, kGroupM, tm, tn);
+  const int idx = (blockIdx.x * 256 + threadIdx.x) * 4;
+  if (idx >= BM * BN) return;
+  const size_t tile_elems = (size_t)BM * BN;
+  const float* first = p.partial + (size_t)tl * p.ksplit * tile_elems;
+  f32x4 v = *(const f32x4*)(first + idx);
+  for (int q = 1; q < p.ksplit; ++q) {
+    const f32x4 w = *(const f32x4*)(first + (size_t)q * tile_elems + idx);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] += w[e];
+  }
+  const int m = tm * BM + idx / BN;
+  if (m >= p.M) return;
+  const float rs = p.row_scale ? p.row_scale[m] : 1.0f;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int n = tn * BN + idx % BN + e;
+    if (n >= p.N) continue;
+    const float bv = p.bias ? read_elem(p.bias, p.out_dtype, n) : 0.0f;
+    write_elem(p.y, p.out_dtype, (size_t)m * p.N + n, v[e] * rs + bv);
+  }
+}
+
+// x [M, K] (fp32 / fp16 / bf16) -> x16 [M, K] fp16 scaled by 2^-e_m per row, row_scale[m] = 2^e_m,
+// with e_m chosen so that max |x16| lies in [2^14, 2^15): every bf16 value maps exactly (fp16
+// keeps 11 mantissa bits), and no row can overflow fp16. One workgroup per row; 8 elements per
+// thread and step (16-byte loads for 16-bit inputs), the row read twice (max, then convert; the
+// second read hits L2).
+template <int DT>
+__global__ __launch_bounds__(256) void rows_to_scaled_f16_kernel(const void* __restrict__ x,
+                                                                 _Float16* __restrict__ x16,
+                                                                 float* __restrict__ row_scale, int K) {
+  __shared__ float red[4];
+  const int row = blockIdx.x;
+  const size_t base = (size_t)row * K;
+  auto load8 = [&](int k, float (&v)[8]) {
+    if constexpr (DT == kF32) {
+      const u32x4 lo = *(const u32x4*)((const float*)x + base + k);
+      const u32x4 hi = *(const u32x4*)((const float*)x + base + k + 4);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t a = lo[e], b = hi[e];
+        v[e] = __builtin_bit_cast(float, a);
+        v[4 + e] = __builtin_bit_cast(float, b);
+      }
+    } else {
+      const u32x4 w = *(const u32x4*)((const uint16_t*)x + base + k);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t word = w[e];
+        v[2 * e] = DT == kBF16 ? bf16_bits_to_f32(word & 0xFFFFu) : f16_bits_to_f32(word & 0xFFFFu);
+        v[2 * e + 1] = DT == kBF16 ? bf16_bits_to_f32(word >> 16) : f16_bits_to_f32(word >> 16);
+      }
+    }
+  };
+  float amax = 0.0f;
+  for (int k = threadIdx.x * 8; k < K; k += 256 * 8) {
+    float v[8];
+    load8(k, v);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, kWave));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  int e = 0;
+  if (amax > 0.0f && amax <= 3.0e38f) {
+    int E;
+    frexpf(amax, &E);  // amax = f * 2^E, f in [0.5, 1)
+    e = E - 15;
+  }
+  if (threadIdx.x == 0) row_scale[row] = ldexpf(1.0f, e);
+  for (int k = threadIdx.x * 8; k < K; k += 256 * 8) {
+    float v[8];
+    load8(k, v);
+    u32x4 out;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) out[q] = pack2_f16(ldexpf(v[2 * q], -e), ldexpf(v[2 * q + 1], -e));
+    *(u32x4*)(x16 + base + k) = out;
+  }
 }
 
 }  // namespace
 
 // ---- host-side launch ------------------------------------------------------------------------
-template <bool kBf16, int WM, int WN, int NWM, int NWN>
-static hipError_t launch_cfg(const W4A16Params& p, int grid, hipStream_t stream) {
-  hipLaunchKernelGGL((w4a16_gemm_kernel<kBf16, WM, WN, NWM, NWN>), dim3(grid), dim3(64 * NWM * NWN), 0,
-                     stream, p);
+// A staging through registers for tiles up to 128 rows (the LDS-DMA path makes the compiler
+// wait for operand reads with lgkmcnt(0)); 256-row tiles keep the DMA path (no registers left).
+#ifndef QL_A_REG_MAX_WM
+#define QL_A_REG_MAX_WM 8
+#endif
+
+template <bool kBf16, int WM>
+static hipError_t launch_cfg(const W4A16Params& p, hipStream_t stream) {
+  constexpr int BM = 16 * WM, BN = 16 * 4 * kWaves;
+  constexpr bool kRegA = WM <= QL_A_REG_MAX_WM;
+  const int tiles = p.tiles_m * p.tiles_n;
+  if (p.dp_tiles > 0)
+    hipLaunchKernelGGL((w4a16_gemm_kernel<kBf16, WM, 4, false, kRegA>), dim3(p.dp_tiles), dim3(64 * kWaves), 0,
+                       stream, p);
+  const int cut = tiles - p.dp_tiles;
+  if (cut > 0) {
+    hipLaunchKernelGGL((w4a16_gemm_kernel<kBf16, WM, 4, true, kRegA>), dim3(cut * p.ksplit), dim3(64 * kWaves), 0,
+                       stream, p);
+    hipLaunchKernelGGL(w4a16_reduce_kernel, dim3((BM * BN + 1023) / 1024, cut), dim3(256), 0, stream, p, BM, BN);
+  }
   return hipGetLastError();
 }
 
 const W4A16Config& w4a16_config(int id) {
-  // {id, BM, BN}
+  // {id, BM, BN}; every config is 4 waves side by side, each 16*WM rows x 64 columns
   static const W4A16Config cfgs[] = {
-      {0, 256, 256},  // WM 16, WN 4, 1 x 4 waves
+      {0, 256, 256},  // WM 16
       {1, 128, 256},  // WM 8
       {2, 64, 256},   // WM 4
       {3, 16, 256},   // WM 1
@@ -267,11 +384,10 @@ const W4A16Config& w4a16_config(int id) {
   return cfgs[id];
 }
 
-hipError_t w4a16_launch(int cfg, bool bf16, const W4A16Params& p, int grid, hipStream_t stream) {
-#define QL_CASE(ID, WM)                                                   \
-  case ID:                                                                \
-    return bf16 ? launch_cfg<true, WM, 4, 1, 4>(p, grid, stream)          \
-                : launch_cfg<false, WM, 4, 1, 4>(p, grid, stream);
+hipError_t w4a16_launch(int cfg, bool bf16, const W4A16Params& p, hipStream_t stream) {
+#define QL_CASE(ID, WM) \
+  case ID:              \
+    return bf16 ? launch_cfg<true, WM>(p, stream) : launch_cfg<false, WM>(p, stream);
   switch (cfg) {
     QL_CASE(0, 16)
     QL_CASE(1, 8)
@@ -281,6 +397,26 @@ hipError_t w4a16_launch(int cfg, bool bf16, const W4A16Params& p, int grid, hipS
       return hipErrorInvalidValue;
   }
 #undef QL_CASE
+}
+
+hipError_t rows_to_scaled_f16_launch(int dtype, const void* x, void* x16, float* row_scale, int64_t M,
+                                     int64_t K, hipStream_t stream) {
+  const dim3 grid((unsigned)M);
+  switch (dtype) {
+    case kF32:
+      hipLaunchKernelGGL(rows_to_scaled_f16_kernel<kF32>, grid, dim3(256), 0, stream, x, (_Float16*)x16, row_scale,
+                         (int)K);
+      break;
+    case kF16:
+      hipLaunchKernelGGL(rows_to_scaled_f16_kernel<kF16>, grid, dim3(256), 0, stream, x, (_Float16*)x16, row_scale,
+                         (int)K);
+      break;
+    default:
+      hipLaunchKernelGGL(rows_to_scaled_f16_kernel<kBF16>, grid, dim3(256), 0, stream, x, (_Float16*)x16,
+                         row_scale, (int)K);
+      break;
+  }
+  return hipGetLastError();
 }
 
 }  // namespace qlinear

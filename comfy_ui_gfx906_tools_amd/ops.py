@@ -135,15 +135,15 @@ def int4_linear(x: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.Tensor, 
     """x [..., K] -> [..., N] in x.dtype: x @ dequant(w_packed, w_scale)^T (+ bias) on the gfx950
     W4A16 kernel. w_packed/w_scale come from quantize_pack_int4 of the weight, folded through the
     same rotation when rotation_group != 0; bias, if given, is already x.dtype (ops.py:167-183).
-    fp32 activations are fed to the MFMA as bf16 (output stays fp32)."""
+    bf16 and fp32 activations (the rotated path is fp32) are staged as exactly row-scaled fp16,
+    so the weights dequantize to fp16 (11-bit mantissa) rather than bf16."""
     shape = x.shape
     K = shape[-1]
     x2d = x.reshape(-1, K)
     if rotation_group:
         R = get_group_rotation(K, rotation_group, x2d.device)
         x2d = apply_group_rotation(x2d.float(), R, rotation_group)
-    mm_dtype = x.dtype if x.dtype in (torch.bfloat16, torch.float16) else torch.bfloat16
-    out = _lib.w4a16_gemm(x2d.to(mm_dtype), w_packed, w_scale, bias, out_dtype=x.dtype)
+    out = _lib.w4a16_gemm(x2d, w_packed, w_scale, bias, out_dtype=x.dtype)
     return out.reshape(*shape[:-1], w_packed.shape[0])
 
 

@@ -53,25 +53,39 @@ int qlinear_abi_version(void);
  * Replaces the pair ext.quantize_int4 + ext.gemm_int4 that int4_linear calls
  * (nodes/ComfyUI-Gfx906Int4/ops.py:181-182; csrc/binding.cpp:53-112; dispatchers
  * csrc/int4_gemm_scaled.hip:248-269): the activation is not quantized here, the weight is
- * dequantized in registers and fed to bf16/fp16 MFMA with fp32 accumulation.
- *   x_dtype   QL_BF16 or QL_F16 (the MFMA operand type)
+ * dequantized in registers and fed to 16-bit MFMA with fp32 accumulation.
+ *   x_dtype   QL_F16: fp16 MFMA on x as given; if row_scale is not NULL, row m of the product
+ *             is multiplied by row_scale[m] in the epilogue (x as written by qlinear_rows_to_f16).
+ *             QL_BF16 / QL_F32: by default each row of x is first scaled by an exact power of
+ *             two into an fp16 copy (in the workspace, as qlinear_rows_to_f16 does) and the
+ *             weights dequantize to fp16 -- 8x less weight rounding than bf16 -- and the
+ *             epilogue scales back exactly. With QL_W4A16_BF16_MFMA in flags, bf16 x is fed to
+ *             bf16 MFMA directly (the reference's own bf16 dequant-then-matmul numerics; no
+ *             staging pass). row_scale must be NULL for these dtypes.
  *   out_dtype QL_F32, QL_F16 or QL_BF16; bias (optional, may be NULL) has dtype out_dtype
  *   K % 32 == 0, K >= 32; M >= 0 (M == 0 launches nothing)
- *   splits    0 = automatic (the engine picks split-K / stream-K for under-filled grids),
- *             1 = one workgroup per output tile, 2..64 = that many workgroups per tile.
- *   workspace device memory of qlinear_w4a16_workspace_bytes(...) bytes whose first
- *             QL_W4A16_COUNTER_BYTES bytes were zeroed once when it was allocated (the kernels
- *             leave them zero again); may be NULL when that size is 0. Calls sharing one
- *             workspace must be ordered (same stream).
+ *   splits    0 = automatic (under-filled last waves are cut into K pieces),
+ *             1 = one workgroup per output tile, 2..64 = that many K pieces per tile.
+ *   workspace device memory of qlinear_w4a16_workspace_bytes(...) bytes (NULL when that is 0),
+ *             scratch for the fp16 staging copy and split-K partial tiles; no initial contents
+ *             needed. Calls sharing one workspace must be ordered (same stream).
  * ------------------------------------------------------------------------------------- */
-#define QL_W4A16_COUNTER_BYTES 65536u /* fixed: counters of at most 16384 cut tiles */
+#define QL_W4A16_BF16_MFMA 1 /* flags bit, see above */
 
-size_t qlinear_w4a16_workspace_bytes(int64_t M, int64_t N, int64_t K, int splits, int device);
+size_t qlinear_w4a16_workspace_bytes(int x_dtype, int64_t M, int64_t N, int64_t K, int splits,
+                                     int flags, int device);
 
-int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const void* w_q4,
-                       const float* w_scale, const void* bias, void* y, int64_t M, int64_t N,
-                       int64_t K, int splits, void* workspace, size_t workspace_bytes,
-                       void* stream);
+int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const float* row_scale,
+                       const void* w_q4, const float* w_scale, const void* bias, void* y,
+                       int64_t M, int64_t N, int64_t K, int splits, int flags, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
+/* Staging pass of the fp16 route: x[M,K] (fp32/fp16/bf16, K % 8 == 0) -> x16[M,K] fp16 with
+ * row m scaled by 2^-e_m, row_scale[m] = 2^e_m, e_m chosen so max|x16[m,:]| is in [2^14, 2^15)
+ * (exact for bf16 and fp16 inputs). No counterpart in the reference, whose activations go to
+ * int4 instead (csrc/int4_gemm_scaled.hip:193-220). */
+int qlinear_rows_to_f16(int x_dtype, const void* x, void* x16, float* row_scale, int64_t M,
+                        int64_t K, void* stream);
 
 /* Number of workgroups per output tile that splits == 0 resolves to; mirrors
  * ext.gemm_int4_auto_splits (csrc/binding.cpp:36-43, 359-362). */

@@ -23,9 +23,9 @@ def _lib():
     return _lib
 
 
-def _run(x, wq, ws, bias=None, out_dtype=torch.float32, splits=0):
+def _run(x, wq, ws, bias=None, out_dtype=torch.float32, splits=0, bf16_mfma=False):
     return _lib().w4a16_gemm(x.to(DEV), wq.to(DEV), ws.to(DEV), None if bias is None else bias.to(DEV),
-                             out_dtype=out_dtype, splits=splits)
+                             out_dtype=out_dtype, splits=splits, bf16_mfma=bf16_mfma)
 
 
 SMALL = [
@@ -81,6 +81,29 @@ def test_w4a16_split_k_and_determinism(splits):
     assert torch.equal(y1, y2), "split-K result is not deterministic"
     ref = orc.w4a16_reference(to_np_f32(x), wq.numpy(), ws.numpy(), bias.numpy())
     assert rel_max_err(to_np_f32(y1), ref) <= TOL
+
+
+@pytest.mark.parametrize("M,N,K", [(7, 300, 512), (130, 640, 3072)])
+def test_w4a16_bf16_mfma_matches_reference_bf16_path(M, N, K):
+    """bf16 MFMA mode against the reference's own W4A16 path for a bf16 model: the dequantized
+    weight cast back to bf16 (nodes.py:52, 116), then the matmul with fp32 accumulation. Only the
+    fp32 summation order differs, so the gate is tight."""
+    x, wq, ws = seeded_linear(M, N, K, seed=21)
+    y = to_np_f32(_run(x, wq, ws, bf16_mfma=True))
+    w_bf16 = orc.round_to_bf16(orc.dequant_int4(wq.numpy(), ws.numpy())).astype(np.float64)
+    ref = to_np_f32(x).astype(np.float64) @ w_bf16.T
+    assert rel_max_err(y, ref) <= 2e-5
+
+
+def test_w4a16_fp32_activations():
+    """fp32 x (the rotated path of int4_linear) goes through the fp16 staging: gate as fp32-dequant."""
+    M, N, K = 33, 256, 1024
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(M, K, generator=g)
+    _, wq, ws = seeded_linear(M, N, K, seed=13)
+    y = to_np_f32(_run(x, wq, ws))
+    ref = orc.w4a16_reference(x.numpy(), wq.numpy(), ws.numpy())
+    assert rel_max_err(y, ref) <= TOL
 
 
 def test_w4a16_exact_on_integer_grid():
