@@ -93,9 +93,10 @@ def _stream_ptr(device: torch.device) -> int:
 
 
 class _Workspaces:
-    """Zero-initialised device workspaces, one per (device, stream): calls that share one must
-    be ordered, and work on one stream is. Grown on demand; the kernels leave the counter
-    area zero after every call."""
+    """Device workspaces, one per (device, stream): calls that share one must be ordered, and
+    work on one stream is. Grown on demand. Every call writes the parts of the workspace it
+    reads (staged activations, row scales, split-K partial tiles) before reading them, so the
+    memory needs no initialisation."""
 
     def __init__(self):
         self._bufs: dict[tuple[int, int], torch.Tensor] = {}
@@ -106,7 +107,7 @@ class _Workspaces:
         with self._lock:
             buf = self._bufs.get(key)
             if buf is None or buf.numel() < nbytes:
-                buf = torch.zeros(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
+                buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, device=device)
                 self._bufs[key] = buf
             return buf
 

@@ -1,0 +1,126 @@
+"""The C ABI on the CPU: libqlinear.so loads, exports every function include/qlinear.h declares
+with the arity the header gives, the ctypes table matches the header, and the argument checks
+that run before any HIP call return the documented status codes and messages. No entry point
+here reaches a device query or a launch (there is no GPU in this container)."""
+import ctypes
+import os
+import re
+import subprocess
+
+import pytest
+
+from tests.conftest import ROOT
+
+HEADER = os.path.join(ROOT, "include", "qlinear.h")
+LIB = os.path.join(ROOT, "comfy_ui_gfx906_tools_amd", "libqlinear.so")
+
+QL_OK, QL_ERR_ARG, QL_ERR_SHAPE, QL_ERR_DTYPE, QL_ERR_ALIGN = 0, 1, 2, 3, 4
+
+
+def _header_functions():
+    """name -> number of parameters, parsed from the prototypes in include/qlinear.h."""
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    out = {}
+    for m in re.finditer(r"\b(?:int|size_t|const char\*)\s+(qlinear_\w+)\s*\(([^)]*)\)\s*;", text):
+        params = m.group(2).strip()
+        out[m.group(1)] = 0 if params in ("", "void") else len(params.split(","))
+    return out
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(LIB):
+        pytest.skip("libqlinear.so not built (python -m comfy_ui_gfx906_tools_amd.build)")
+    from comfy_ui_gfx906_tools_amd import _lib
+    return _lib.load_library(LIB)
+
+
+def test_header_parses():
+    fns = _header_functions()
+    assert {"qlinear_w4a16_gemm", "qlinear_w8a8_gemm", "qlinear_quantize_int4", "qlinear_last_error"} <= set(fns)
+    assert fns["qlinear_w4a16_gemm"] == 16 and fns["qlinear_abi_version"] == 0
+
+
+def test_every_declared_symbol_is_exported(lib):
+    fns = _header_functions()
+    dyn = subprocess.run(["nm", "-D", "--defined-only", LIB], capture_output=True, text=True, check=True).stdout
+    exported = {line.split()[-1] for line in dyn.splitlines() if " T " in line}
+    missing = sorted(set(fns) - exported)
+    assert not missing, f"declared in include/qlinear.h but not exported: {missing}"
+    for name in fns:
+        assert getattr(lib, name) is not None
+
+
+def test_ctypes_table_matches_header(lib):
+    from comfy_ui_gfx906_tools_amd import _lib
+    fns = _header_functions()
+    assert set(_lib.SIGNATURES) == set(fns)
+    for name, (_, args) in _lib.SIGNATURES.items():
+        assert len(args) == fns[name], name
+
+
+def test_abi_version_and_error_text(lib):
+    assert lib.qlinear_abi_version() >> 16 == 1
+    assert isinstance(lib.qlinear_last_error(), bytes)
+
+
+def _err(lib):
+    return lib.qlinear_last_error().decode()
+
+
+def test_w4a16_argument_checks(lib):
+    f = lib.qlinear_w4a16_gemm
+    # bad activation dtype (int32)
+    assert f(3, 0, None, None, None, None, None, None, 4, 64, 64, 0, 0, None, 0, None) == QL_ERR_DTYPE
+    assert "x dtype" in _err(lib)
+    assert f(2, 3, None, None, None, None, None, None, 4, 64, 64, 0, 0, None, 0, None) == QL_ERR_DTYPE
+    # K not a multiple of the 32-wide group
+    assert f(2, 2, None, None, None, None, None, None, 4, 64, 48, 0, 0, None, 0, None) == QL_ERR_SHAPE
+    assert "K % 32 == 0" in _err(lib) and "K=48" in _err(lib)
+    assert f(2, 2, None, None, None, None, None, None, 4, 0, 64, 0, 0, None, 0, None) == QL_ERR_SHAPE
+    assert f(2, 2, None, None, None, None, None, None, 4, 64, 64, 65, 0, None, 0, None) == QL_ERR_ARG
+    assert f(2, 2, None, None, None, None, None, None, 4, 64, 64, 0, 4, None, 0, None) == QL_ERR_ARG
+    # row scales are only meaningful for fp16 activations staged by qlinear_rows_to_f16
+    assert f(2, 2, None, ctypes.c_void_p(16), None, None, None, None, 4, 64, 64, 0, 0, None, 0, None) == QL_ERR_ARG
+    # M == 0 is a no-op that succeeds (binding.cpp:64, 93 of the reference return empty outputs)
+    assert f(2, 2, None, None, None, None, None, None, 0, 64, 64, 0, 0, None, 0, None) == QL_OK
+    assert f(2, 2, None, None, None, None, None, None, 4, 64, 64, 0, 0, None, 0, None) == QL_ERR_ARG
+    assert "null" in _err(lib)
+    assert f(1, 2, ctypes.c_void_p(8), None, ctypes.c_void_p(16), ctypes.c_void_p(16), None, ctypes.c_void_p(16),
+             4, 64, 64, 0, 0, None, 0, None) == QL_ERR_ALIGN
+
+
+def test_quantizer_and_w8a8_argument_checks(lib):
+    assert lib.qlinear_quantize_int4(2, 2, None, None, None, 4, 64, None) == QL_ERR_ARG
+    assert lib.qlinear_quantize_int4(2, 0, None, None, None, 4, 40, None) == QL_ERR_SHAPE
+    assert lib.qlinear_quantize_int4(3, 0, None, None, None, 4, 64, None) == QL_ERR_DTYPE
+    assert lib.qlinear_quantize_int4(2, 0, None, None, None, 0, 64, None) == QL_OK
+    assert lib.qlinear_quantize_int8_per_token(3, None, None, None, 4, 64, None) == QL_ERR_DTYPE
+    assert lib.qlinear_quantize_int8_per_token(2, None, None, None, 4, 64, None) == QL_ERR_ARG
+    assert lib.qlinear_w8a8_gemm(2, None, None, None, None, None, None, 4, 64, 96, None) == QL_ERR_SHAPE
+    assert "K % 64 == 0" in _err(lib)
+    assert lib.qlinear_w8a8_gemm(7, None, None, None, None, None, None, 4, 64, 128, None) == QL_ERR_DTYPE
+    assert lib.qlinear_w8a8_gemm(2, None, None, None, None, None, None, 0, 64, 128, None) == QL_OK
+    assert lib.qlinear_w8a8_gemm(2, ctypes.c_void_p(16), None, ctypes.c_void_p(16), None, None, ctypes.c_void_p(16),
+                                 4, 64, 128, None) == QL_ERR_ARG  # float output needs both scale vectors
+    assert lib.qlinear_rows_to_f16(2, None, None, None, 4, 12, None) == QL_ERR_SHAPE
+    assert lib.qlinear_rows_to_f16(3, None, None, None, 4, 16, None) == QL_ERR_DTYPE
+
+
+def test_error_text_is_per_thread(lib):
+    import threading
+    assert lib.qlinear_quantize_int4(3, 0, None, None, None, 4, 64, None) == QL_ERR_DTYPE
+    main_msg = _err(lib)
+    seen = {}
+
+    def other():
+        seen["before"] = lib.qlinear_last_error().decode()
+        lib.qlinear_w8a8_gemm(2, None, None, None, None, None, None, 4, 64, 96, None)
+        seen["after"] = lib.qlinear_last_error().decode()
+
+    t = threading.Thread(target=other)
+    t.start()
+    t.join()
+    assert seen["before"] == "" and "K % 64" in seen["after"]
+    assert _err(lib) == main_msg
