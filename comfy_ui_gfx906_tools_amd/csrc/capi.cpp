@@ -145,8 +145,10 @@ int check_w4a16_shape(int64_t M, int64_t N, int64_t K) {
   if (M < 0 || N <= 0 || K < 32 || K % 32 != 0)
     return fail(QL_ERR_SHAPE, "expected x [M, K], w_q4 [N, K/2], w_scale [N, K/32] with K %% 32 == 0, K >= 32, N > 0; "
                 "got M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
-  if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || K > INT32_MAX / 2)
-    return fail(QL_ERR_SHAPE, "dimension too large: M=%lld N=%lld K=%lld", (long long)M, (long long)N, (long long)K);
+  // the kernels address one tile's rows of x (up to 256 x K fp16) with 32-bit buffer offsets
+  if (M > INT32_MAX / 2 || N > INT32_MAX / 2 || K > (1 << 22))
+    return fail(QL_ERR_SHAPE, "dimension too large: M=%lld N=%lld K=%lld (K <= 4194304)", (long long)M, (long long)N,
+                (long long)K);
   return QL_OK;
 }
 

@@ -59,6 +59,22 @@ __device__ __forceinline__ void write_elem(void* p, int dt, size_t i, float v) {
   }
 }
 
+// ---- compile-time loops ----------------------------------------------------------------------
+// static_for<B, E>(f) calls f(std::integral_constant<int, i>{}) for i = B .. E-1 as straight-line
+// code: the index is a constant expression inside f, so register arrays indexed by it stay in
+// registers whatever the compiler's unrolling heuristics decide about loop size.
+template <int I>
+struct ic {
+  static constexpr int value = I;
+};
+template <int B, int E, typename F>
+__device__ __forceinline__ void static_for(F&& f) {
+  if constexpr (B < E) {
+    f(ic<B>{});
+    static_for<B + 1, E>(f);
+  }
+}
+
 // ---- int4 -> 16-bit dequant in registers ---------------------------------------------------
 // One packed dword holds 8 consecutive K elements: nibble t (bits 4t..4t+3) is element t,
 // two's complement (the reference's packing, ops.py:119-121). Returns the 8 values q*s
@@ -103,11 +119,48 @@ __device__ __forceinline__ i32x4 mfma16_i8(u32x4 a, u32x4 b, i32x4 c) {
 __device__ __forceinline__ void load_lds16(const void* gptr, void* lds_base) {
   __builtin_amdgcn_global_load_lds(gptr, (__attribute__((address_space(3))) void*)lds_base, 16, 0, 0);
 }
+// ---- raw buffer loads ------------------------------------------------------------------------
+// A buffer resource covers [base, base + bytes); a load whose offset (per-lane voffset + wave-uniform
+// soffset) lies at or past `bytes` returns zeros instead of touching memory. The kernels use this
+// for every edge (rows past M, columns past N, K past the end) and advance through K by bumping
+// the scalar offset, so no per-stage vector address arithmetic is needed.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr int kRsrcWord3 = 0x00020000;      // gfx9 V# word 3: 32-bit data format, raw access
+constexpr uint32_t kOobOffset = 0x80000000u;  // voffset that is out of range for every resource here
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kRsrcWord3);
+}
+__device__ __forceinline__ u32x4 buf_load16(rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_amdgcn_raw_buffer_load_b128(r, voff, soff, 0);
+}
+__device__ __forceinline__ float buf_load_f32(rsrc_t r, uint32_t voff, uint32_t soff) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, voff, soff, 0));
+}
+
+// Buffer load of 16 B per lane straight into LDS (buffer_load_dwordx4 ... lds): lane i of the wave
+// writes lds_base + 16*i; lds_base must be wave-uniform. Out-of-range lanes write zeros.
+__device__ __forceinline__ void buf_load16_lds(rsrc_t r, void* lds_base, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_base, 16, voff, soff, 0,
+                                           0);
+}
+
 // s_waitcnt as a real instruction (not inline asm), so the compiler's own wait insertion knows
 // which counters are already drained. gfx9 encoding: vmcnt [3:0]+[15:14], expcnt [6:4],
 // lgkmcnt [11:8]; a field at its maximum means "do not wait" on that counter.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }   // vmcnt(0)
 __device__ __forceinline__ void wait_lgkm() { __builtin_amdgcn_s_waitcnt(0xC07F); }   // lgkmcnt(0)
+
+// ---- LDS layout of 256-byte operand rows ----------------------------------------------------
+// A stage row is 16 chunks of 16 B; logical chunk c of row r is stored in slot c ^ lds_swz(r & 15).
+// An MFMA operand read (ds_read_b128) has lane l fetch row l % 16, chunk 4 * (l / 16) + i. The LDS
+// serves such a read 32 lanes (512 B, all 128 banks) at a time, so the 32 chunks of lanes 0-31
+// (rows 0-15, chunk blocks 0 and 1; likewise 32-63) must land in 32 distinct 16-byte bank
+// groups of the 512-byte line formed by rows r and r ^ 1. lds_swz is the bit permutation
+// (r1 r2 r0 r3) of r: the 8 rows of one parity then use chunk offsets that are distinct and never
+// differ by 4 (the gap between chunk blocks 0 and 1), and all 16 rows together are still
+// conflict-free for 16-lane (256 B) service.
+__device__ __forceinline__ int lds_swz(int r) { return ((r >> 1) & 3) | ((r & 1) << 2) | (r & 8); }
 
 // ---- workgroup -> tile order ---------------------------------------------------------------
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2). Renumber them

@@ -4,21 +4,31 @@
 //
 // The reference computes this product as dequantize-then-matmul (nodes.py:43-52, 116) and its
 // production kernel is a W4A4 v_dot8 GEMM (csrc/int4_gemm_scaled.hip:53-180); neither is the
-// shape of this kernel. Design, per 256-thread workgroup (4 waves side by side along N) and a
-// BM x BN output tile:
+// shape of this kernel. Design, per 256-thread workgroup (4 waves side by side along N, one wave
+// per SIMD) and a BM x 256 output tile:
 //
-// * A (activations) is staged HBM -> LDS with global_load_lds_dwordx4, 128 K per stage, double
-//   buffered in two distinct arrays. A row of a stage is 256 B = 16 chunks of 16 B; chunk c of
-//   row r sits at slot c ^ (r & 15), so the 16 rows an MFMA operand read touches hit 16
-//   distinct bank groups. Rows past M are clamped to row M-1 (their outputs are never stored);
-//   K past the end is clamped to the last chunk and meets zero weights.
+// * The cost that bounds this kernel is instruction issue: a SIMD issues one VALU or MFMA
+//   instruction per 4 cycles, and one v_mfma_f32_16x16x32 occupies the matrix core for 16, so a
+//   wave has 3 VALU slots per MFMA. The int4 -> 16-bit dequant costs 19 VALU per 8 weights, paid
+//   once per weight per workgroup, so its cost per MFMA falls with the tile height: 2.4 VALU per
+//   MFMA at BM = 128, 1.2 at BM = 256 (the large-M tile).
+// * All global reads are raw buffer loads: a per-lane offset fixed for the whole K loop plus a
+//   scalar offset bumped per stage, so the loop has no vector address arithmetic; rows past M,
+//   columns past N and K past the end fall outside the buffer range and read as zeros.
+// * A (activations): 128 K per stage, staged HBM -> registers -> LDS, double buffered in two
+//   distinct LDS arrays. A row of a stage is 256 B = 16 chunks of 16 B; chunk c of row r sits
+//   at slot c ^ lds_swz(r & 15), so an MFMA operand read is free of bank conflicts.
 // * B (weights) never touches LDS. Lane (c = l%16, j = l/16) of a wave loads 16 B of weight row
 //   n = col0 + c: the whole 32-element quant group j of the stage, with its one scale, and
 //   dequantizes it in registers (dequant8: int4 -> q*s -> fp16/bf16). The MFMA K-slot map is
 //   permuted to match: MFMA i of a stage takes, in K-slot block j, elements 32j + 8i .. +7; A is
 //   read from LDS with the same map (chunk 4j + i), so every lane's load is one group.
-// * Each wave owns a (16*WM) x (16*WN) sub-tile of 16x16 accumulators (v_mfma_f32_16x16x32).
-//   With WM = 16 the dequant costs 0.5 element per MFMA.
+// * Each wave owns a (16*WM) x 64 sub-tile of 16x16 accumulators (v_mfma_f32_16x16x32).
+// * Pipeline, per stage s: issue the global loads of stage s+1 (B first, then A); run the
+//   stage's MFMAs with operand reads kD fragments ahead and the next K-step's dequant spread
+//   between them; kD fragments before the end, store the staged A of s+1 to the other LDS
+//   buffer, dequantize K-step 0 of s+1, pass the workgroup barrier and issue the first operand
+//   reads of s+1 -- the stage's last MFMAs then cover both the barrier and the read latency.
 // * Optional row scales (the fp16 route for bf16 activations): x arrives pre-scaled per row by
 //   2^-e (exact) and the epilogue multiplies by 2^e (exact).
 // * Scheduling: every workgroup runs one K range of one tile. The first dp_tiles tiles are
@@ -39,17 +49,21 @@ constexpr int kRowBytes = 256;      // one A row of a stage
 constexpr int kGroupsPerStage = 4;  // 128 / 32
 constexpr int kGroupM = 8;
 constexpr int kWaves = 4;
+constexpr int kWN = 4;              // 16-column blocks per wave
 
-template <bool kBf16, int WM, int WN, bool kCut, bool kRegA>
+template <bool kBf16, int WM, bool kCut, bool kKTail>
 __global__ __launch_bounds__(64 * kWaves) void w4a16_gemm_kernel(W4A16Params p) {
+  constexpr int WN = kWN;
   constexpr int BM = 16 * WM;
   constexpr int BN = 16 * WN * kWaves;
   constexpr int kStageBytes = BM * kRowBytes;
-  constexpr int kBlocksPerWave = BM / 4 / kWaves;  // 1 KiB LDS blocks each wave fills per stage
-  static_assert(BM % (4 * kWaves) == 0, "A tile must split into whole 1 KiB blocks per wave");
+  constexpr int kLoadsA = BM / 16;        // 1 KiB (4-row) blocks each wave stages per stage
+  constexpr int kQ = 4 * WM;              // operand fragments per stage: 4 K-steps x WM row blocks
+  constexpr int kD = WM < 3 ? WM : 3;     // operand read-ahead, in fragments
+  constexpr int kR = kD + 1;              // operand register ring
+  static_assert(kQ % kR == 0, "the operand ring must restart at every stage");
   // Two distinct arrays (not one indexed by stage parity): the compiler's alias analysis then
-  // sees that operand reads of one buffer never touch the DMA target of the other, and does not
-  // wait for the next stage's loads before the current stage's MFMAs.
+  // sees that operand reads of one buffer never touch the stores into the other.
   __shared__ __attribute__((aligned(1024))) uint8_t lds0[kStageBytes];
   __shared__ __attribute__((aligned(1024))) uint8_t lds1[kStageBytes];
 
@@ -59,8 +73,6 @@ __global__ __launch_bounds__(64 * kWaves) void w4a16_gemm_kernel(W4A16Params p) 
   const int M = p.M, N = p.N, K = p.K;
   const int groups = K / kGroup;
   const int S = p.stages;  // steps of two stages
-
-  const uint16_t* __restrict__ x = (const uint16_t*)p.x;
 
   // ---- this workgroup's segment ----------------------------------------------------------
   const int g = xcd_remap(blockIdx.x, gridDim.x);
@@ -79,142 +91,142 @@ __global__ __launch_bounds__(64 * kWaves) void w4a16_gemm_kernel(W4A16Params p) 
   tile_coords(t, p.tiles_m, p.tiles_n, kGroupM, tm, tn);
   const int m0 = tm * BM, n0 = tn * BN;
 
-  // ---- B addressing ------------------------------------------------------------------------
-  const uint8_t* bptr[WN];
-  const float* sptr[WN];
-  bool bok[WN];
+  // ---- buffer resources and per-lane offsets ----------------------------------------------
+  // Per-lane offsets are fixed for the whole K loop; the stage (and, for A, the 16-row group of
+  // the load, for B / scales the 16-column block) goes into the scalar offset.
+  const int rows = min(M - m0, BM), cols = min(N - n0, BN);
+  const rsrc_t rs_a = make_rsrc((const uint16_t*)p.x + (size_t)m0 * K, (uint32_t)rows * K * 2);
+  const rsrc_t rs_b = make_rsrc((const uint8_t*)p.wq + (size_t)n0 * (K / 2), (uint32_t)cols * (K / 2));
+  const rsrc_t rs_s = make_rsrc(p.ws + (size_t)n0 * groups, (uint32_t)cols * groups * 4);
+  // A: wave wn stages rows [wn*BM/4, (wn+1)*BM/4) in kLoadsA loads of 4 rows; load q covers row
+  // wn*BM/4 + 4q + j4, whose swizzle depends on q % 4 only
+  constexpr int kVoA = kLoadsA < 4 ? kLoadsA : 4;
+  uint32_t vo_a[kVoA];
+  auto a_row = [&](int q) { return (wn * kLoadsA + q) * 4 + j4; };
+  auto a_lch = [&](int q) { return r16 ^ lds_swz(a_row(q) & 15); };
 #pragma unroll
-  for (int fn = 0; fn < WN; ++fn) {
-    const int n = n0 + (wn * WN + fn) * 16 + r16;
-    bok[fn] = n < N;
-    const int nc = min(n, N - 1);
-    bptr[fn] = (const uint8_t*)p.wq + (size_t)nc * (K / 2);
-    sptr[fn] = p.ws + (size_t)nc * groups;
-  }
+  for (int q = 0; q < kVoA; ++q) vo_a[q] = (uint32_t)(a_row(q) * K + a_lch(q) * 8) * 2;
+  const uint32_t a_q4_step = 16u * K * 2;  // four loads further down = 16 rows
+  const int col0 = wn * WN * 16 + r16;
+  const uint32_t vo_b = (uint32_t)col0 * (K / 2) + j4 * 16;
+  const uint32_t vo_s = ((uint32_t)col0 * groups + j4) * 4;
+  const uint32_t b_fn_step = 16u * (K / 2), s_fn_step = 16u * groups * 4;
 
-  // A staging, either HBM -> LDS directly (global_load_lds_dwordx4) or through registers
-  // (global_load_dwordx4, then ds_write_b128 at the end of the stage). Same LDS layout.
-  u32x4 areg[kRegA ? kBlocksPerWave : 1];
-  auto a_src = [&](int s, int q) {
-    const int blk = wn * kBlocksPerWave + q;
-    const int row = blk * 4 + j4;
-    const int lch = r16 ^ (row & 15);
-    const int gm = min(m0 + row, M - 1);
-    const int gk = min(s * kStageK + lch * 8, K - 8);
-    return x + (size_t)gm * K + gk;
-  };
-  auto issue_a = [&](int s, uint8_t* buf) {
-#pragma unroll
-    for (int q = 0; q < kBlocksPerWave; ++q) {
-      if constexpr (kRegA) {
-        areg[q] = *(const u32x4*)a_src(s, q);
-      } else {
-        load_lds16(a_src(s, q), buf + (wn * kBlocksPerWave + q) * 1024);
-      }
+  // Global loads of stage s: B (raw int4 + scales) into registers first, then A straight into
+  // the LDS buffer `dst`. With kKTail (K not a multiple of 256) a stage that reaches past K masks
+  // the chunks / groups past the end with an out-of-range offset. `live` false turns every load
+  // into an out-of-range one (a stage past the segment): no memory traffic, no branch.
+  const rsrc_t rs_none = make_rsrc(p.ws, 0);
+  auto load_stage = [&](int s, bool live, u32x4 (&raw)[WN], float (&sc)[WN], uint8_t* dst) {
+    const rsrc_t ra = live ? rs_a : rs_none, rb = live ? rs_b : rs_none, rsc = live ? rs_s : rs_none;
+    uint32_t vb = vo_b, vs = vo_s;
+    if constexpr (kKTail) {
+      const bool gok = s * kGroupsPerStage + j4 < groups;
+      vb = gok ? vb : kOobOffset;
+      vs = gok ? vs : kOobOffset;
     }
-  };
-  auto commit_a = [&](uint8_t* buf) {
-    if constexpr (kRegA) {
-#pragma unroll
-      for (int q = 0; q < kBlocksPerWave; ++q) *(u32x4*)(buf + (wn * kBlocksPerWave + q) * 1024 + lane * 16) = areg[q];
-    }
-  };
-  // Raw loads only; the zero-scale select for columns past N / groups past K is applied by the
-  // stage that consumes them, so no wait is forced right after the loads are issued.
-  auto load_b = [&](int s, u32x4 (&raw)[WN], float (&sc)[WN]) {
-    const int kgc = min(s * kGroupsPerStage + j4, groups - 1);
 #pragma unroll
     for (int fn = 0; fn < WN; ++fn) {
-      raw[fn] = *(const u32x4*)(bptr[fn] + (size_t)kgc * 16);
-      sc[fn] = sptr[fn][kgc];
+      raw[fn] = buf_load16(rb, vb, s * 64 + fn * b_fn_step);
+      sc[fn] = buf_load_f32(rsc, vs, s * 16 + fn * s_fn_step);
+    }
+#pragma unroll
+    for (int q = 0; q < kLoadsA; ++q) {
+      uint32_t va = vo_a[q % kVoA];
+      if constexpr (kKTail) va = s * kStageK + a_lch(q) * 8 < K ? va : kOobOffset;
+      buf_load16_lds(ra, dst + (wn * kLoadsA + q) * 1024, va, s * 256 + (q / 4) * a_q4_step);
     }
   };
+  // operand fragment q = i * WM + fm of a stage: rows fm*16 + (l % 16), K-step i (chunk 4j + i).
+  // One lane address per (buffer, K-step); the row block is the instruction's immediate offset.
+  uint32_t fbase[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) fbase[i] = r16 * kRowBytes + (((4 * j4 + i) ^ lds_swz(r16)) * 16);
+  auto frag = [&](const uint8_t* buf, int q) {
+    const int i = q / WM, fm = q % WM;
+    return *(const u32x4*)(buf + fbase[i] + fm * 16 * kRowBytes);
+  };
 
+  // Accumulators start as the result of an MFMA on zeros rather than as a plain zero constant:
+  // the compiler then keeps them in AGPRs across the K loop instead of copying every one between
+  // AGPRs and VGPRs at each loop iteration.
   f32x4 acc[WM][WN];
 #pragma unroll
   for (int fm = 0; fm < WM; ++fm)
 #pragma unroll
-    for (int fn = 0; fn < WN; ++fn) acc[fm][fn] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int fn = 0; fn < WN; ++fn)
+      acc[fm][fn] = mfma16<kBf16>(u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}, f32x4{0.f, 0.f, 0.f, 0.f});
 
   // Two register sets for the raw weights, alternating with the two LDS buffers.
   u32x4 rawA[WN], rawB[WN];
   float scA[WN], scB[WN];
+  u32x4 b[WN], bn[WN];  // dequantized weights of the current / the next K-step
+  u32x4 ar[kR];         // operand ring
 
-  // One pipeline stage: operands of stage s are in `cur` (LDS) and raw/scr (registers); stage s+1
-  // is fetched into `nxt` and raw_n/sc_n. Order matters: the stage's own registers are consumed
-  // (first dequant, first operand reads) before the next loads are issued, so the waits the
-  // compiler places for them never also wait for the next stage's loads.
+  // One pipeline stage. Entering: `cur` holds A of stage s (published by the last barrier),
+  // raw/scr the weights of s, bn the dequantized K-step 0 of s, ar[0..kD-1] the first kD
+  // operand fragments of s (reads issued). Fragment q sits in ring slot q % kR.
   auto stage = [&](int s, int s_end, const uint8_t* cur, uint8_t* nxt, u32x4 (&raw)[WN], float (&scr)[WN],
                    u32x4 (&raw_n)[WN], float (&sc_n)[WN]) {
-    wait_vmem();
-    __syncthreads();
-    float sc[WN], neg8s[WN];
-    const bool kok = s * kGroupsPerStage + j4 < groups;
+    load_stage(s + 1, s + 1 < s_end, raw_n, sc_n, nxt);
+    float neg8s[WN];
 #pragma unroll
-    for (int fn = 0; fn < WN; ++fn) {
-      sc[fn] = (bok[fn] && kok) ? scr[fn] : 0.0f;  // zero scale -> exact zero weights
-      neg8s[fn] = -8.0f * sc[fn];
-    }
-    u32x4 b[WN];
-#pragma unroll
-    for (int fn = 0; fn < WN; ++fn) b[fn] = dequant8<kBf16>(raw[fn][0], sc[fn], neg8s[fn]);
-
-    // A operand blocks q = i * WM + fm (K-step i, 16-row block fm); ring of three registers,
-    // reads issued two blocks ahead of their MFMAs
-    const uint8_t* abase = cur + r16 * kRowBytes;
-    auto a_addr = [&](int q) {
-      const int i = q / WM, fm = q % WM;
-      return (const u32x4*)(abase + fm * 16 * kRowBytes + (((4 * j4 + i) ^ r16) * 16));
-    };
-    constexpr int kBlocks = 4 * WM;
-    u32x4 ar[3];
-    ar[0] = *a_addr(0);
-    if (kBlocks > 1) ar[1] = *a_addr(1);
-    __builtin_amdgcn_sched_barrier(0);
-
-    if (s + 1 < s_end) {
-      issue_a(s + 1, nxt);
-      load_b(s + 1, raw_n, sc_n);
-    }
-
-    u32x4 bn[WN];
-#pragma unroll
-    for (int q = 0; q < kBlocks; ++q) {
-      const int i = q / WM, fm = q % WM;
-      if (q + 2 < kBlocks) ar[(q + 2) % 3] = *a_addr(q + 2);
-      if (fm == 0 && i > 0) {
+    for (int fn = 0; fn < WN; ++fn) neg8s[fn] = -8.0f * scr[fn];
+    static_for<0, kQ>([&](auto qc) {
+      constexpr int q = decltype(qc)::value;
+      constexpr int i = q / WM, fm = q % WM;
+      if constexpr (fm == 0) {
 #pragma unroll
         for (int fn = 0; fn < WN; ++fn) b[fn] = bn[fn];
       }
+      if constexpr (q == kQ - kD) {
+        // hand-over to stage s+1: its K-step 0 dequantized, its A (loaded into the other buffer
+        // since the start of this stage) complete, the barrier; from here the ring reads the
+        // first fragments of s+1, and the MFMAs q .. kQ-1 of this stage cover the barrier and
+        // their latency
 #pragma unroll
-      for (int fn = 0; fn < WN; ++fn) acc[fm][fn] = mfma16<kBf16>(ar[q % 3], b[fn], acc[fm][fn]);
-      // dequant of K-step i+1, spread over the 16-row blocks: column block fn goes with row
-      // block fn % WM (all of them with the first row block when WM == 1)
-      if (i < 3) {
+        for (int fn = 0; fn < WN; ++fn) bn[fn] = dequant8<kBf16>(raw_n[fn][0], sc_n[fn], -8.0f * sc_n[fn]);
+        wait_vmem();  // this wave's A loads of s+1 have landed in LDS
+        __syncthreads();
+      }
+      if constexpr (q + kD < kQ) {
+        ar[(q + kD) % kR] = frag(cur, q + kD);
+      } else {
+        ar[(q + kD) % kR] = frag(nxt, q + kD - kQ);  // past the segment: read, never used
+      }
+#pragma unroll
+      for (int fn = 0; fn < WN; ++fn) acc[fm][fn] = mfma16<kBf16>(b[fn], ar[q % kR], acc[fm][fn]);
+      // dequant of K-step i+1, spread over the row blocks of K-step i
+      if constexpr (i < 3) {
 #pragma unroll
         for (int fn = 0; fn < WN; ++fn)
-          if (fn % WM == fm) bn[fn] = dequant8<kBf16>(raw[fn][i + 1], sc[fn], neg8s[fn]);
+          if ((WM >= 4 ? fn * (WM / 4) : fn % WM) == fm) bn[fn] = dequant8<kBf16>(raw[fn][i + 1], scr[fn], neg8s[fn]);
       }
       __builtin_amdgcn_sched_barrier(0);
-    }
-    if (s + 1 < s_end) commit_a(nxt);
+    });
   };
+
+  // ---- prologue: stage 2*s0 loaded, staged, dequantized, published --------------------------
+  const int s_end = 2 * s1;
+  load_stage(2 * s0, true, rawA, scA, lds0);
+  wait_vmem();
+#pragma unroll
+  for (int fn = 0; fn < WN; ++fn) bn[fn] = dequant8<kBf16>(rawA[fn][0], scA[fn], -8.0f * scA[fn]);
+  __syncthreads();
+#pragma unroll
+  for (int d = 0; d < kD; ++d) ar[d] = frag(lds0, d);
 
   // Segments are counted in steps of two stages (256 K), so both halves of the unrolled loop
   // body run unconditionally and the accumulators stay in one register class.
-  const int s_end = 2 * s1;
-  issue_a(2 * s0, lds0);
-  commit_a(lds0);
-  load_b(2 * s0, rawA, scA);
-  // Drain the kernel-argument scalar loads: with none pending, the compiler can wait for LDS
-  // operand reads with partial lgkmcnt counts instead of lgkmcnt(0).
-  wait_lgkm();
   for (int sp = s0; sp < s1; ++sp) {
     stage(2 * sp, s_end, lds0, lds1, rawA, scA, rawB, scB);
     stage(2 * sp + 1, s_end, lds1, lds0, rawB, scB, rawA, scA);
   }
 
   // ---- epilogue ----------------------------------------------------------------------------
+  // The MFMAs take the weights as their first operand, so each 16x16 block holds y^T: lane l has
+  // y[m][n .. n+3] for m = block row + l % 16, n = block column + 4 * (l / 16) -- four adjacent
+  // outputs, stored with one 8-byte (16-bit out) or 16-byte (fp32 out) store.
   // A whole tile goes to y (row scale, bias, out dtype); a cut tile's piece goes as plain fp32 to
   // its partial slot, a tile-local [BM][BN] array. Same store loop for both.
   void* dst = p.y;
@@ -231,25 +243,41 @@ __global__ __launch_bounds__(64 * kWaves) void w4a16_gemm_kernel(W4A16Params p) 
     bias = nullptr;
     row_scale = nullptr;
   }
-  float bv[WN];
+  const bool vec = dst_N % 4 == 0 && ((uintptr_t)dst & 15) == 0;
+  float bv[WN][4];
 #pragma unroll
   for (int fn = 0; fn < WN; ++fn) {
-    const int n = dst_n0 + (wn * WN + fn) * 16 + r16;
-    bv[fn] = (bias && n < dst_N) ? read_elem(bias, dst_dtype, n) : 0.0f;
+    const int n = dst_n0 + (wn * WN + fn) * 16 + 4 * j4;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) bv[fn][e] = (bias && n + e < dst_N) ? read_elem(bias, p.out_dtype, n + e) : 0.0f;
   }
-  // one 16-row block at a time, fenced, so the row scales and addresses of all rows are never
-  // live together
 #pragma unroll
   for (int fm = 0; fm < WM; ++fm) {
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int m = dst_m0 + fm * 16 + 4 * j4 + e;
-      if (m >= dst_M) continue;
+    const int m = dst_m0 + fm * 16 + r16;
+    if (m < dst_M) {
       const float rs = row_scale ? row_scale[m] : 1.0f;
 #pragma unroll
       for (int fn = 0; fn < WN; ++fn) {
-        const int n = dst_n0 + (wn * WN + fn) * 16 + r16;
-        if (n < dst_N) write_elem(dst, dst_dtype, (size_t)m * dst_N + n, acc[fm][fn][e] * rs + bv[fn]);
+        const int n = dst_n0 + (wn * WN + fn) * 16 + 4 * j4;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) v[e] = acc[fm][fn][e] * rs + bv[fn][e];
+        const size_t off = (size_t)m * dst_N + n;
+        if (vec && n + 3 < dst_N) {
+          if (dst_dtype == kF32) {
+            *(f32x4*)((float*)dst + off) = f32x4{v[0], v[1], v[2], v[3]};
+          } else {
+            typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+            const bool bf = dst_dtype == kBF16;
+            const u32x2 w = {bf ? pack2_bf16(v[0], v[1]) : pack2_f16(v[0], v[1]),
+                             bf ? pack2_bf16(v[2], v[3]) : pack2_f16(v[2], v[3])};
+            *(u32x2*)((uint16_t*)dst + off) = w;
+          }
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            if (n + e < dst_N) write_elem(dst, dst_dtype, off + e, v[e]);
+        }
       }
     }
     __builtin_amdgcn_sched_barrier(0);
@@ -350,27 +378,26 @@ __global__ __launch_bounds__(256) void rows_to_scaled_f16_kernel(const void* __r
 }  // namespace
 
 // ---- host-side launch ------------------------------------------------------------------------
-// A staging through registers for tiles up to 128 rows (the LDS-DMA path makes the compiler
-// wait for operand reads with lgkmcnt(0)); 256-row tiles keep the DMA path (no registers left).
-#ifndef QL_A_REG_MAX_WM
-#define QL_A_REG_MAX_WM 8
-#endif
-
-template <bool kBf16, int WM>
+template <bool kBf16, int WM, bool kKTail>
 static hipError_t launch_cfg(const W4A16Params& p, hipStream_t stream) {
-  constexpr int BM = 16 * WM, BN = 16 * 4 * kWaves;
-  constexpr bool kRegA = WM <= QL_A_REG_MAX_WM;
+  constexpr int BM = 16 * WM, BN = 16 * kWN * kWaves;
   const int tiles = p.tiles_m * p.tiles_n;
   if (p.dp_tiles > 0)
-    hipLaunchKernelGGL((w4a16_gemm_kernel<kBf16, WM, 4, false, kRegA>), dim3(p.dp_tiles), dim3(64 * kWaves), 0,
-                       stream, p);
+    hipLaunchKernelGGL((w4a16_gemm_kernel<kBf16, WM, false, kKTail>), dim3(p.dp_tiles), dim3(64 * kWaves), 0, stream,
+                       p);
   const int cut = tiles - p.dp_tiles;
   if (cut > 0) {
-    hipLaunchKernelGGL((w4a16_gemm_kernel<kBf16, WM, 4, true, kRegA>), dim3(cut * p.ksplit), dim3(64 * kWaves), 0,
+    hipLaunchKernelGGL((w4a16_gemm_kernel<kBf16, WM, true, kKTail>), dim3(cut * p.ksplit), dim3(64 * kWaves), 0,
                        stream, p);
     hipLaunchKernelGGL(w4a16_reduce_kernel, dim3((BM * BN + 1023) / 1024, cut), dim3(256), 0, stream, p, BM, BN);
   }
   return hipGetLastError();
+}
+
+template <bool kBf16, int WM>
+static hipError_t launch_k(const W4A16Params& p, hipStream_t stream) {
+  // K a multiple of 256 (two full stages per loop step): no K masking in the loads
+  return p.K % 256 == 0 ? launch_cfg<kBf16, WM, false>(p, stream) : launch_cfg<kBf16, WM, true>(p, stream);
 }
 
 const W4A16Config& w4a16_config(int id) {
@@ -387,7 +414,7 @@ const W4A16Config& w4a16_config(int id) {
 hipError_t w4a16_launch(int cfg, bool bf16, const W4A16Params& p, hipStream_t stream) {
 #define QL_CASE(ID, WM) \
   case ID:              \
-    return bf16 ? launch_cfg<true, WM>(p, stream) : launch_cfg<false, WM>(p, stream);
+    return bf16 ? launch_k<true, WM>(p, stream) : launch_k<false, WM>(p, stream);
   switch (cfg) {
     QL_CASE(0, 16)
     QL_CASE(1, 8)

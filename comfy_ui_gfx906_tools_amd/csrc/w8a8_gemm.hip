@@ -55,7 +55,7 @@ __global__ __launch_bounds__(64 * NWM * NWN) void w8a8_gemm_kernel(W8A8Params p)
     for (int q = 0; q < kBlocksPerWave; ++q) {
       const int blk = wave * kBlocksPerWave + q;
       const int row = blk * 4 + j4;
-      const int lch = r16 ^ (row & 15);
+      const int lch = r16 ^ lds_swz(row & 15);
       const int gm = min(m0 + row, M - 1);
       const int gk = min(s * kStageK8 + lch * 16, K - 16);
       load_lds16(p.xq + (size_t)gm * K + gk, lds + buf * kStageBytes + blk * 1024);
@@ -99,7 +99,7 @@ __global__ __launch_bounds__(64 * NWM * NWN) void w8a8_gemm_kernel(W8A8Params p)
     const uint8_t* abase = lds + buf * kStageBytes + (wm * WM * 16 + r16) * kRowBytes8;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int pch = (4 * j4 + i) ^ r16;
+      const int pch = (4 * j4 + i) ^ lds_swz(r16);
 #pragma unroll
       for (int fm = 0; fm < WM; ++fm) {
         const u32x4 a = *(const u32x4*)(abase + fm * 16 * kRowBytes8 + pch * 16);
