@@ -103,7 +103,7 @@ W4A16Plan plan_w4a16(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, i
   pl.BN = c.BN;
   pl.tiles_m = (int)((M + c.BM - 1) / c.BM);
   pl.tiles_n = (int)((N + c.BN - 1) / c.BN);
-  pl.stages = (int)((K + 255) / 256);  // steps of two 128-K pipeline stages
+  pl.stages = w4a16_steps(pl.cfg, K);  // K loop steps of the config's pipeline
   const int tiles = pl.tiles_m * pl.tiles_n;
   pl.dp_tiles = tiles;
   pl.ksplit = 1;

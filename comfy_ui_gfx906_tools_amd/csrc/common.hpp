@@ -149,6 +149,12 @@ __device__ __forceinline__ void buf_load16_lds(rsrc_t r, void* lds_base, uint32_
 // which counters are already drained. gfx9 encoding: vmcnt [3:0]+[15:14], expcnt [6:4],
 // lgkmcnt [11:8]; a field at its maximum means "do not wait" on that counter.
 __device__ __forceinline__ void wait_vmem() { __builtin_amdgcn_s_waitcnt(0x0F70); }   // vmcnt(0)
+// vmcnt(N): at most N vector-memory instructions of this wave still outstanding (in issue order)
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is a 6-bit field");
+  __builtin_amdgcn_s_waitcnt((N & 0xF) | ((N >> 4) << 14) | 0x0F70);
+}
 __device__ __forceinline__ void wait_lgkm() { __builtin_amdgcn_s_waitcnt(0xC07F); }   // lgkmcnt(0)
 
 // ---- LDS layout of 256-byte operand rows ----------------------------------------------------
@@ -161,6 +167,16 @@ __device__ __forceinline__ void wait_lgkm() { __builtin_amdgcn_s_waitcnt(0xC07F)
 // differ by 4 (the gap between chunk blocks 0 and 1), and all 16 rows together are still
 // conflict-free for 16-lane (256 B) service.
 __device__ __forceinline__ int lds_swz(int r) { return ((r >> 1) & 3) | ((r & 1) << 2) | (r & 8); }
+
+// Workgroup barrier without the memory fence of __syncthreads(): the fence would also wait for
+// every outstanding global load (vmcnt(0)), including prefetches meant to stay in flight across
+// the barrier. Callers wait for exactly what the barrier publishes (wait_vmcnt / wait_lgkm)
+// first; the empty asm statements keep the compiler from moving memory accesses across it.
+__device__ __forceinline__ void barrier_no_fence() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
 
 // ---- workgroup -> tile order ---------------------------------------------------------------
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2). Renumber them

@@ -18,7 +18,7 @@ struct W4A16Params {
   int M, N, K;
   int out_dtype;
   int tiles_m, tiles_n;
-  int stages;            // ceil(K / 256): steps of two 128-K pipeline stages
+  int stages;            // K loop steps: ceil(K / (128 * w4a16_nbuf(WM)))
   int dp_tiles;          // tiles processed whole, one workgroup each
   int ksplit;            // K pieces of every tile past dp_tiles (>= 2 when any)
 };
@@ -26,6 +26,12 @@ struct W4A16Params {
 struct W4A16Config {
   int id, BM, BN;
 };
+
+// LDS stage buffers of the W4A16 kernel for a tile of 16*WM rows: three (loads two stages ahead)
+// while they fit, two for 256-row tiles.
+constexpr int w4a16_nbuf(int WM) { return WM >= 16 ? 2 : 3; }
+// K loop steps (of w4a16_nbuf stages of 128 K) for config `cfg`
+int w4a16_steps(int cfg, int64_t K);
 
 const W4A16Config& w4a16_config(int id);
 hipError_t w4a16_launch(int cfg, bool bf16, const W4A16Params& p, hipStream_t stream);

@@ -62,17 +62,20 @@ __global__ __launch_bounds__(64 * kWaves) void w4a16_gemm_kernel(W4A16Params p) 
   constexpr int kD = WM < 3 ? WM : 3;     // operand read-ahead, in fragments
   constexpr int kR = kD + 1;              // operand register ring
   static_assert(kQ % kR == 0, "the operand ring must restart at every stage");
-  // Two distinct arrays (not one indexed by stage parity): the compiler's alias analysis then
-  // sees that operand reads of one buffer never touch the stores into the other.
-  __shared__ __attribute__((aligned(1024))) uint8_t lds0[kStageBytes];
-  __shared__ __attribute__((aligned(1024))) uint8_t lds1[kStageBytes];
+  // kNB stage buffers in a ring, loads issued kNB-1 stages ahead: three for tiles up to 128 rows
+  // (96 KiB of LDS), two for 256-row tiles (3 x 64 KiB would exceed the 160 KiB of a CU).
+  constexpr int kNB = w4a16_nbuf(WM);
+  constexpr int kLoadsPerStage = 2 * WN + kLoadsA;  // vmem instructions of one load_stage
+  constexpr bool kRolled = kNB == 2;
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kNB * kStageBytes];
 
   const int lane = threadIdx.x & 63;
   const int wn = threadIdx.x >> 6;
   const int r16 = lane & 15, j4 = lane >> 4;
   const int M = p.M, N = p.N, K = p.K;
   const int groups = K / kGroup;
-  const int S = p.stages;  // steps of two stages
+  const int S = p.stages;                      // loop steps of kNB stages
+  const int s_real = (K + kStageK - 1) / kStageK;  // stages that hold data
 
   // ---- this workgroup's segment ----------------------------------------------------------
   const int g = xcd_remap(blockIdx.x, gridDim.x);
@@ -112,39 +115,55 @@ __global__ __launch_bounds__(64 * kWaves) void w4a16_gemm_kernel(W4A16Params p) 
   const uint32_t vo_s = ((uint32_t)col0 * groups + j4) * 4;
   const uint32_t b_fn_step = 16u * (K / 2), s_fn_step = 16u * groups * 4;
 
-  // Global loads of stage s: B (raw int4 + scales) into registers first, then A straight into
-  // the LDS buffer `dst`. With kKTail (K not a multiple of 256) a stage that reaches past K masks
-  // the chunks / groups past the end with an out-of-range offset. `live` false turns every load
-  // into an out-of-range one (a stage past the segment): no memory traffic, no branch.
+  // Global loads of stage s: B (raw int4 + scales) into registers, then A straight into the LDS
+  // buffer `dst`, one vector-memory instruction per call (index l < kLoadsPerStage), so a stage's
+  // loads can be spread between MFMAs: issued in one burst they fill the address FIFO of the
+  // CU's texture unit and the wave, which issues in order, stalls its MFMAs behind them. With
+  // kKTail (K not a multiple of 128) a stage that reaches past K masks the chunks / groups past
+  // the end with an out-of-range offset. `live` false turns every load into an out-of-range one
+  // (a stage past the segment): no memory traffic, no branch.
   const rsrc_t rs_none = make_rsrc(p.ws, 0);
-  auto load_stage = [&](int s, bool live, u32x4 (&raw)[WN], float (&sc)[WN], uint8_t* dst) {
-    const rsrc_t ra = live ? rs_a : rs_none, rb = live ? rs_b : rs_none, rsc = live ? rs_s : rs_none;
-    uint32_t vb = vo_b, vs = vo_s;
-    if constexpr (kKTail) {
-      const bool gok = s * kGroupsPerStage + j4 < groups;
-      vb = gok ? vb : kOobOffset;
-      vs = gok ? vs : kOobOffset;
-    }
-#pragma unroll
-    for (int fn = 0; fn < WN; ++fn) {
-      raw[fn] = buf_load16(rb, vb, s * 64 + fn * b_fn_step);
-      sc[fn] = buf_load_f32(rsc, vs, s * 16 + fn * s_fn_step);
-    }
-#pragma unroll
-    for (int q = 0; q < kLoadsA; ++q) {
+  auto load_one = [&](int l, int s, bool live, u32x4 (&raw)[WN], float (&sc)[WN], uint8_t* dst) {
+    if (l < 2 * WN) {
+      uint32_t vb = vo_b, vs = vo_s;
+      if constexpr (kKTail) {
+        const bool gok = s * kGroupsPerStage + j4 < groups;
+        vb = gok ? vb : kOobOffset;
+        vs = gok ? vs : kOobOffset;
+      }
+      if (l < WN) {
+        raw[l] = buf_load16(live ? rs_b : rs_none, vb, s * 64 + l * b_fn_step);
+      } else {
+        sc[l - WN] = buf_load_f32(live ? rs_s : rs_none, vs, s * 16 + (l - WN) * s_fn_step);
+      }
+    } else {
+      const int q = l - 2 * WN;
       uint32_t va = vo_a[q % kVoA];
       if constexpr (kKTail) va = s * kStageK + a_lch(q) * 8 < K ? va : kOobOffset;
-      buf_load16_lds(ra, dst + (wn * kLoadsA + q) * 1024, va, s * 256 + (q / 4) * a_q4_step);
+      buf_load16_lds(live ? rs_a : rs_none, dst + (wn * kLoadsA + q) * 1024, va, s * 256 + (q / 4) * a_q4_step);
     }
   };
-  // operand fragment q = i * WM + fm of a stage: rows fm*16 + (l % 16), K-step i (chunk 4j + i).
-  // One lane address per (buffer, K-step); the row block is the instruction's immediate offset.
-  uint32_t fbase[4];
+  auto load_stage = [&](int s, bool live, u32x4 (&raw)[WN], float (&sc)[WN], uint8_t* dst) {
 #pragma unroll
-  for (int i = 0; i < 4; ++i) fbase[i] = r16 * kRowBytes + (((4 * j4 + i) ^ lds_swz(r16)) * 16);
-  auto frag = [&](const uint8_t* buf, int q) {
+    for (int l = 0; l < kLoadsPerStage; ++l) load_one(l, s, live, raw, sc, dst);
+  };
+  // operand fragment q = i * WM + fm of a stage: rows fm*16 + (l % 16), K-step i (chunk 4j + i).
+  // One lane address per (buffer, K-step), kept opaque to the optimizer so it does not fold the
+  // buffer offset into the immediate (which tops out at 64 KiB) and materialize an address per
+  // fragment; the row block fm*4 KiB is the ds_read immediate.
+  typedef __attribute__((address_space(3))) const u32x4* lds_frag_ptr;
+  const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds;
+  uint32_t fbase[kNB][4];
+#pragma unroll
+  for (int k = 0; k < kNB; ++k)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      fbase[k][i] = lds_base + k * kStageBytes + r16 * kRowBytes + (((4 * j4 + i) ^ lds_swz(r16)) * 16);
+      asm volatile("" : "+v"(fbase[k][i]));
+    }
+  auto frag = [&](int k, int q) {
     const int i = q / WM, fm = q % WM;
-    return *(const u32x4*)(buf + fbase[i] + fm * 16 * kRowBytes);
+    return *(lds_frag_ptr)(fbase[k][i] + fm * 16 * kRowBytes);
   };
 
   // Accumulators start as the result of an MFMA on zeros rather than as a plain zero constant:
@@ -157,21 +176,41 @@ __global__ __launch_bounds__(64 * kWaves) void w4a16_gemm_kernel(W4A16Params p) 
     for (int fn = 0; fn < WN; ++fn)
       acc[fm][fn] = mfma16<kBf16>(u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}, f32x4{0.f, 0.f, 0.f, 0.f});
 
-  // Two register sets for the raw weights, alternating with the two LDS buffers.
-  u32x4 rawA[WN], rawB[WN];
-  float scA[WN], scB[WN];
+  // kNB register sets for the raw weights, rotating with the LDS buffers.
+  u32x4 raw[kNB][WN];
+  float sc[kNB][WN];
   u32x4 b[WN], bn[WN];  // dequantized weights of the current / the next K-step
   u32x4 ar[kR];         // operand ring
 
-  // One pipeline stage. Entering: `cur` holds A of stage s (published by the last barrier),
-  // raw/scr the weights of s, bn the dequantized K-step 0 of s, ar[0..kD-1] the first kD
-  // operand fragments of s (reads issued). Fragment q sits in ring slot q % kR.
-  auto stage = [&](int s, int s_end, const uint8_t* cur, uint8_t* nxt, u32x4 (&raw)[WN], float (&scr)[WN],
-                   u32x4 (&raw_n)[WN], float (&sc_n)[WN]) {
-    load_stage(s + 1, s + 1 < s_end, raw_n, sc_n, nxt);
+  // One pipeline stage s, held in ring slot k = s % kNB. Entering: buffer k holds A of stage s
+  // (published by the last barrier), raw[k]/sc[k] its weights, bn its dequantized K-step 0,
+  // ar[0..kD-1] its first kD operand fragments (reads issued); the loads of stages s+1 ..
+  // s+kNB-2 are in flight. Fragment q sits in ring slot q % kR.
+  // Unrolled (kc = ring slot as a constant): the loop body holds kNB stages with fixed slots.
+  // Rolled (kRolled, two buffers, 256-row tiles): one stage per loop iteration; the LDS slot is a
+  // runtime value (per-stage base addresses fcur / fnxt), the weights of s+1 land in raw[1] and
+  // move to raw[0] at the end. 256 accumulators leave the register allocator no spare AGPRs, and
+  // a two-stage loop body makes it shuffle them between stages; one stage per iteration does not.
+  auto stage = [&](auto kc, int s, int s_end) {
+    constexpr int k = kRolled ? 0 : decltype(kc)::value;
+    constexpr int k1 = kRolled ? 1 : (k + 1) % kNB, kl = kRolled ? 1 : (k + kNB - 1) % kNB;
+    const int s_load = s + kNB - 1;
+    const bool live = s_load < s_end;
+    const int slot = kRolled ? (s & 1) : k;  // LDS buffer of stage s
+    uint32_t fcur[4], fnxt[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      fcur[i] = kRolled ? fbase[0][i] + slot * kStageBytes : fbase[k][i];
+      fnxt[i] = kRolled ? fbase[0][i] + (slot ^ 1) * kStageBytes : fbase[k1 % kNB][i];
+    }
+    auto fragb = [&](const uint32_t (&fb)[4], int q) {
+      const int i = q / WM, fm = q % WM;
+      return *(lds_frag_ptr)(fb[i] + fm * 16 * kRowBytes);
+    };
+    uint8_t* const ldst = lds + (kRolled ? (slot ^ 1) : kl) * kStageBytes;  // target of the loads
     float neg8s[WN];
 #pragma unroll
-    for (int fn = 0; fn < WN; ++fn) neg8s[fn] = -8.0f * scr[fn];
+    for (int fn = 0; fn < WN; ++fn) neg8s[fn] = -8.0f * sc[k][fn];
     static_for<0, kQ>([&](auto qc) {
       constexpr int q = decltype(qc)::value;
       constexpr int i = q / WM, fm = q % WM;
@@ -179,20 +218,29 @@ __global__ __launch_bounds__(64 * kWaves) void w4a16_gemm_kernel(W4A16Params p) 
 #pragma unroll
         for (int fn = 0; fn < WN; ++fn) b[fn] = bn[fn];
       }
+      // this step's share of the loads of stage s+kNB-1, spread over the first kLoadWindow steps
+      // (all before the hand-over; with two buffers in the first half, as the hand-over waits
+      // for them)
+      constexpr int kLoadWindow = kNB == 2 ? kQ / 2 : kQ - kD;
+      static_for<0, kLoadsPerStage>([&](auto lc) {
+        constexpr int l = decltype(lc)::value;
+        if constexpr (l * kLoadWindow / kLoadsPerStage == q)
+          load_one(l, s_load, live, raw[kl], sc[kl], ldst);
+      });
       if constexpr (q == kQ - kD) {
-        // hand-over to stage s+1: its K-step 0 dequantized, its A (loaded into the other buffer
-        // since the start of this stage) complete, the barrier; from here the ring reads the
-        // first fragments of s+1, and the MFMAs q .. kQ-1 of this stage cover the barrier and
-        // their latency
+        // hand-over to stage s+1: its K-step 0 dequantized, its A (loaded into buffer k1 since
+        // kNB-2 stages ago) complete, the barrier; from here the ring reads the first fragments
+        // of s+1, and the MFMAs q .. kQ-1 of this stage cover the barrier and their latency
 #pragma unroll
-        for (int fn = 0; fn < WN; ++fn) bn[fn] = dequant8<kBf16>(raw_n[fn][0], sc_n[fn], -8.0f * sc_n[fn]);
-        wait_vmem();  // this wave's A loads of s+1 have landed in LDS
-        __syncthreads();
+        for (int fn = 0; fn < WN; ++fn) bn[fn] = dequant8<kBf16>(raw[k1][fn][0], sc[k1][fn], -8.0f * sc[k1][fn]);
+        wait_vmcnt<(kNB - 2) * kLoadsPerStage>();  // this wave's loads of s+1 have landed
+        wait_lgkm();                                // its operand reads of buffer k are done
+        barrier_no_fence();
       }
       if constexpr (q + kD < kQ) {
-        ar[(q + kD) % kR] = frag(cur, q + kD);
+        ar[(q + kD) % kR] = fragb(fcur, q + kD);
       } else {
-        ar[(q + kD) % kR] = frag(nxt, q + kD - kQ);  // past the segment: read, never used
+        ar[(q + kD) % kR] = fragb(fnxt, q + kD - kQ);  // past the segment: read, never used
       }
 #pragma unroll
       for (int fn = 0; fn < WN; ++fn) acc[fm][fn] = mfma16<kBf16>(b[fn], ar[q % kR], acc[fm][fn]);
@@ -200,27 +248,42 @@ __global__ __launch_bounds__(64 * kWaves) void w4a16_gemm_kernel(W4A16Params p) 
       if constexpr (i < 3) {
 #pragma unroll
         for (int fn = 0; fn < WN; ++fn)
-          if ((WM >= 4 ? fn * (WM / 4) : fn % WM) == fm) bn[fn] = dequant8<kBf16>(raw[fn][i + 1], scr[fn], neg8s[fn]);
+          if ((WM >= 4 ? fn * (WM / 4) : fn % WM) == fm) bn[fn] = dequant8<kBf16>(raw[k][fn][i + 1], sc[k][fn], neg8s[fn]);
       }
       __builtin_amdgcn_sched_barrier(0);
     });
+    if constexpr (kRolled) {
+#pragma unroll
+      for (int fn = 0; fn < WN; ++fn) {
+        raw[0][fn] = raw[1][fn];
+        sc[0][fn] = sc[1][fn];
+      }
+    }
   };
 
-  // ---- prologue: stage 2*s0 loaded, staged, dequantized, published --------------------------
-  const int s_end = 2 * s1;
-  load_stage(2 * s0, true, rawA, scA, lds0);
-  wait_vmem();
+  // ---- prologue: stages up to kNB-2 ahead in flight, the first one published -----------------
+  // Stages at or past s_end (the segment's end, or the last stage holding data) load nothing.
+  const int s_first = kNB * s0;
+  const int s_end = min(kNB * s1, s_real);
+  static_for<0, kNB - 1>([&](auto kc) {
+    constexpr int k = decltype(kc)::value;
+    load_stage(s_first + k, s_first + k < s_end, raw[k], sc[k], lds + k * kStageBytes);
+  });
+  wait_vmcnt<(kNB - 2) * kLoadsPerStage>();
 #pragma unroll
-  for (int fn = 0; fn < WN; ++fn) bn[fn] = dequant8<kBf16>(rawA[fn][0], scA[fn], -8.0f * scA[fn]);
-  __syncthreads();
+  for (int fn = 0; fn < WN; ++fn) bn[fn] = dequant8<kBf16>(raw[0][fn][0], sc[0][fn], -8.0f * sc[0][fn]);
+  barrier_no_fence();
 #pragma unroll
-  for (int d = 0; d < kD; ++d) ar[d] = frag(lds0, d);
+  for (int d = 0; d < kD; ++d) ar[d] = frag(0, d);
 
-  // Segments are counted in steps of two stages (256 K), so both halves of the unrolled loop
-  // body run unconditionally and the accumulators stay in one register class.
-  for (int sp = s0; sp < s1; ++sp) {
-    stage(2 * sp, s_end, lds0, lds1, rawA, scA, rawB, scB);
-    stage(2 * sp + 1, s_end, lds1, lds0, rawB, scB, rawA, scA);
+  // Segments are counted in steps of kNB stages, so every stage of the unrolled loop body has a
+  // fixed ring slot and the accumulators stay in one register class.
+  if constexpr (kRolled) {
+    for (int st = s_first; st < kNB * s1; ++st) stage(ic<0>{}, st, s_end);
+  } else {
+    for (int sp = s0; sp < s1; ++sp) {
+      static_for<0, kNB>([&](auto kc) { stage(kc, kNB * sp + decltype(kc)::value, s_end); });
+    }
   }
 
   // ---- epilogue ----------------------------------------------------------------------------
@@ -396,8 +459,8 @@ static hipError_t launch_cfg(const W4A16Params& p, hipStream_t stream) {
 
 template <bool kBf16, int WM>
 static hipError_t launch_k(const W4A16Params& p, hipStream_t stream) {
-  // K a multiple of 256 (two full stages per loop step): no K masking in the loads
-  return p.K % 256 == 0 ? launch_cfg<kBf16, WM, false>(p, stream) : launch_cfg<kBf16, WM, true>(p, stream);
+  // K a multiple of 128 (every stage full): no K masking in the loads
+  return p.K % kStageK == 0 ? launch_cfg<kBf16, WM, false>(p, stream) : launch_cfg<kBf16, WM, true>(p, stream);
 }
 
 const W4A16Config& w4a16_config(int id) {
@@ -409,6 +472,12 @@ const W4A16Config& w4a16_config(int id) {
       {3, 16, 256},   // WM 1
   };
   return cfgs[id];
+}
+
+int w4a16_steps(int cfg, int64_t K) {
+  const int wm = w4a16_config(cfg).BM / 16;
+  const int64_t per_step = (int64_t)kStageK * w4a16_nbuf(wm);
+  return (int)((K + per_step - 1) / per_step);
 }
 
 hipError_t w4a16_launch(int cfg, bool bf16, const W4A16Params& p, hipStream_t stream) {
