@@ -1,11 +1,11 @@
 #!/usr/bin/env python3
 """Benchmark of the W4A16 hot path on one MI355X: the Flux-style DiT MLP pair.
 
-One step = fc1 3072->12288 (W4A16, bias) -> GELU-tanh -> fc2 12288->3072 (W4A16, bias) over
-M = 4608 tokens (4096 image + 512 text), bf16 activations, int4 group-32 weights in the
-reference's packed layout, random init (seed 1 = config index), inputs resident in HBM.
-Each linear is the engine's fp16 route: the exact row-scaled fp16 staging pass, then the W4A16
-GEMM kernel. Prints ONE JSON line (the driver's contract) with the whole-step TFLOP/s (2*M*N*K per
+One step = fc1 3072->12288 (W4A16, bias, GELU-tanh fused into its epilogue) -> fc2 12288->3072
+(W4A16, bias) over M = 4608 tokens (4096 image + 512 text), bf16 activations, int4 group-32
+weights in the reference's packed layout, random init (seed 1 = config index), inputs resident in
+HBM. Each linear is the engine's fp16 route: the exact row-scaled fp16 staging pass, then the
+W4A16 GEMM (the 256 x 256-tile kernel at these shapes). Prints ONE JSON line (the driver's contract) with the whole-step TFLOP/s (2*M*N*K per
 GEMM; GELU and staging not counted as flops), the GEMM kernel's MFMA roofline from HIP events
 around its launches, the parity gate of this same run, and the CPU baseline (the oracle's fp32
 dequant-then-matmul path on the host cores).
@@ -118,21 +118,20 @@ def main():
     # current stream, which _lib passes to every entry point)
     gemm_events = {"fc1": [], "fc2": []}
 
-    def linear(a, wq, ws, bias, record, name):
+    def linear(a, wq, ws, bias, record, name, gelu=False):
         a16, rs = _lib.rows_to_f16(a)
         if record:
             e0 = torch.cuda.Event(enable_timing=True)
             e1 = torch.cuda.Event(enable_timing=True)
             e0.record()
-        y = _lib.w4a16_gemm(a16, wq, ws, bias, out_dtype=torch.bfloat16, row_scale=rs)
+        y = _lib.w4a16_gemm(a16, wq, ws, bias, out_dtype=torch.bfloat16, row_scale=rs, gelu=gelu)
         if record:
             e1.record()
             gemm_events[name].append((e0, e1))
         return y
 
     def step(record=False):
-        h = linear(x, w1q, w1s, b1, record, "fc1")
-        h = torch.nn.functional.gelu(h, approximate="tanh")
+        h = linear(x, w1q, w1s, b1, record, "fc1", gelu=True)  # GELU-tanh fused into fc1's epilogue
         return linear(h, w2q, w2s, b2, record, "fc2")
 
     # ---- parity gate of this run (fp32-dequant reference on the GPU, BASELINE tolerance) -----
@@ -161,8 +160,9 @@ def main():
     value = flops_step / (elapsed / args.steps) / 1e12
     avg_ms = {k: sum(a.elapsed_time(b) for a, b in v) / len(v) for k, v in gemm_events.items()}
     flops_launch = 2.0 * M_TOKENS * HIDDEN * MLP  # fc1 and fc2 have the same 2*M*N*K
-    # roofline of the dominant kernel: the fc1 GEMM, one launch of w4a16_gemm_kernel (1728 tiles of
-    # 128 x 256, no K split), the largest single kernel of the step
+    # roofline of the dominant kernel: the fc1 GEMM call (w4a16_tile256_kernel: 768 whole 256 x 256
+    # tiles, then the last 96 tiles as 192 halves of 128 x 256 in a second launch; HIP events around
+    # both), the largest GEMM of the step
     achieved = flops_launch / (avg_ms["fc1"] * 1e-3) / 1e12
 
     traffic = None
@@ -189,7 +189,8 @@ def main():
                    "route": "row-scaled fp16 staging + fp16 MFMA, fp32 accumulate", "parallelism": "single GPU"},
         "roofline": {"bound": "mfma", "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
                      "frac": round(achieved / PEAK_BF16_TFLOPS, 4), "traffic": traffic,
-                     "kernel": "w4a16_gemm_kernel, fc1 launch (M=4608 N=12288 K=3072, 347.9 GFLOP)",
+                     "kernel": "w4a16_tile256_kernel, fc1 GEMM call with fused GELU (M=4608 N=12288 K=3072, "
+                               "347.9 GFLOP)",
                      "avg_launch_ms": round(avg_ms["fc1"], 4)},
         "gemm_ms": {k: round(v, 4) for k, v in avg_ms.items()},
         "parity": {"fc1_max_rel_err": err1, "fc2_max_rel_err": err2, "gate": GATE,

@@ -24,6 +24,9 @@ QL_F32, QL_F16, QL_BF16, QL_I32 = 0, 1, 2, 3
 _DTYPE_CODE = {torch.float32: QL_F32, torch.float16: QL_F16, torch.bfloat16: QL_BF16, torch.int32: QL_I32}
 
 W4A16_BF16_MFMA = 1  # flags: bf16 activations straight into bf16 MFMA (see include/qlinear.h)
+W4A16_GELU_TANH = 2  # flags: fused GELU-tanh epilogue
+W4A16_CFG_SHIFT = 8  # flags bits 8-11: forced kernel configuration + 1 (QL_W4A16_CFG)
+W4A16_TILE256 = 4    # configuration id of the 256 x 256, 8-wave kernel
 
 RULE_DIV = 0    # scale = amax / 7        (torch on CPU)
 RULE_RECIP = 1  # scale = amax * fl(1/7)  (torch on GPU; the reference kernel)
@@ -135,12 +138,15 @@ def rows_to_f16(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
 
 def w4a16_gemm(x: torch.Tensor, w_q4: torch.Tensor, w_scale: torch.Tensor, bias: torch.Tensor | None = None,
                out_dtype: torch.dtype | None = None, splits: int = 0, bf16_mfma: bool = False,
-               row_scale: torch.Tensor | None = None) -> torch.Tensor:
+               row_scale: torch.Tensor | None = None, config: int | None = None,
+               gelu: bool = False) -> torch.Tensor:
     """y[M, N] = x[M, K] @ dequant(w_q4, w_scale)^T (+ bias) on the gfx950 W4A16 kernel.
     x: fp16/bf16/fp32 [M, K]; w_q4: int8 [N, K/2]; w_scale: fp32 [N, K/32]; bias: out_dtype [N].
     bf16 and fp32 activations go through the exact row-scaled fp16 staging unless bf16_mfma is
     set (then bf16 x meets bf16-rounded weights, the reference's bf16 dequant numerics).
-    row_scale (fp16 x only): per-row factor from rows_to_f16, applied in the epilogue."""
+    row_scale (fp16 x only): per-row factor from rows_to_f16, applied in the epilogue.
+    config: force kernel configuration 0-6 (include/qlinear.h, QL_W4A16_CFG); None = automatic.
+    gelu: fused GELU-tanh epilogue (QL_W4A16_GELU_TANH): gelu(round(y)), as Linear -> GELU."""
     lib = load_library()
     x = _dev_tensor(x, "x")
     w_q4 = _dev_tensor(w_q4, "w_q4")
@@ -168,7 +174,9 @@ def w4a16_gemm(x: torch.Tensor, w_q4: torch.Tensor, w_scale: torch.Tensor, bias:
     y = torch.empty((M, N), dtype=out_dtype, device=x.device)
     if M == 0:
         return y
-    flags = W4A16_BF16_MFMA if bf16_mfma else 0
+    flags = (W4A16_BF16_MFMA if bf16_mfma else 0) | (W4A16_GELU_TANH if gelu else 0)
+    if config is not None:
+        flags |= (int(config) + 1) << W4A16_CFG_SHIFT
     xdt = _DTYPE_CODE[x.dtype]
     if row_scale is not None:
         row_scale = _dev_tensor(row_scale, "row_scale")

@@ -81,33 +81,66 @@ struct W4A16Plan {
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
-// Tile height for large M: 128 rows (config 1) or 256 rows (config 0). 128 measures faster:
-// at 256 rows the 256 accumulators leave the compiler no registers to pipeline operand reads.
-#ifndef QL_W4A16_LARGE_CFG
-#define QL_W4A16_LARGE_CFG 1
-#endif
+// Kernel configurations: 0-3 are w4a16_gemm_kernel tiles of 256 / 128 / 64 / 16 rows x 256
+// columns (4 waves side by side); 4-6 are the w4a16_tile256_kernel variants 0-2 (256 x 256
+// tiles, whole tiles, K % 64 == 0). Automatic choice: the smallest tile that covers M for
+// M <= 128, else a 256 x 256 tile when its tiles fill every CU at least once, else 128-row tiles
+// (whose last wave of tiles the planner may cut into K pieces).
+constexpr int kCfgTile256 = 4;
+constexpr int kCfgLast = kCfgTile256 + kTile256Variants - 1;
+constexpr int kCfgTile256Auto = kCfgTile256 + 1;
+bool is_tile256(int cfg) { return cfg >= kCfgTile256 && cfg <= kCfgLast; }
 
-int w4a16_cfg_for(int64_t M) {
+// Tiles of the 256 x 256 kernel that run whole: every full round of CUs; the remaining tiles are
+// cut into 128-row halves when their halves fit in one more round, else they run whole too.
+int64_t tile256_whole(int64_t tiles, int cus) {
+  const int64_t rem = tiles % cus;
+  return (rem > 0 && 2 * rem <= cus) ? tiles - rem : tiles;
+}
+
+// Makespan model in units of one 256 x 256 tile's time on a CU: the 256 x 256 kernel runs its full
+// rounds plus a half-tile round (about 0.6 of a round) or one more whole round; the 128-row kernel
+// balances its tiles over all CUs (K-cut last wave) but spends about 1.3x the time per flop
+// (measured at the BASELINE shapes).
+bool prefer_tile256(int64_t M, int64_t N, int64_t K, int cus) {
+  if (K % 64 != 0) return false;
+  const int64_t tiles = ((M + 255) / 256) * ((N + 255) / 256);
+  const int64_t whole = tile256_whole(tiles, cus);
+  const double t256 = (double)(whole / cus) + (whole < tiles ? 0.6 : (whole % cus ? 1.0 : 0.0));
+  const double t128 = 1.3 * (double)tiles / cus;
+  return t256 <= t128;
+}
+
+// (An explicit K split, splits >= 2, needs the 4-wave kernel: the 256 x 256 kernel has none.)
+int w4a16_cfg_for(int64_t M, int64_t N, int64_t K, int splits, int cus) {
   if (M <= 16) return 3;
   if (M <= 64) return 2;
   if (M <= 128) return 1;
-  return QL_W4A16_LARGE_CFG;
+  return (splits < 2 && prefer_tile256(M, N, K, cus)) ? kCfgTile256Auto : 1;
 }
 
 W4A16Plan plan_w4a16(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, int flags, int cus) {
   W4A16Plan pl{};
   pl.prepass = x_dtype == QL_F32 || (x_dtype == QL_BF16 && !(flags & QL_W4A16_BF16_MFMA));
-  pl.cfg = w4a16_cfg_for(M);
-  const W4A16Config& c = w4a16_config(pl.cfg);
-  pl.BM = c.BM;
-  pl.BN = c.BN;
-  pl.tiles_m = (int)((M + c.BM - 1) / c.BM);
-  pl.tiles_n = (int)((N + c.BN - 1) / c.BN);
-  pl.stages = w4a16_steps(pl.cfg, K);  // K loop steps of the config's pipeline
+  const int forced = (flags & QL_W4A16_CFG_MASK) >> QL_W4A16_CFG_SHIFT;
+  pl.cfg = forced ? forced - 1 : w4a16_cfg_for(M, N, K, splits, cus);
+  if (is_tile256(pl.cfg)) {
+    pl.BM = pl.BN = 256;
+    pl.stages = (int)(K / 64);
+  } else {
+    const W4A16Config& c = w4a16_config(pl.cfg);
+    pl.BM = c.BM;
+    pl.BN = c.BN;
+    pl.stages = w4a16_steps(pl.cfg, K);  // K loop steps of the config's pipeline
+  }
+  pl.tiles_m = (int)((M + pl.BM - 1) / pl.BM);
+  pl.tiles_n = (int)((N + pl.BN - 1) / pl.BN);
   const int tiles = pl.tiles_m * pl.tiles_n;
   pl.dp_tiles = tiles;
   pl.ksplit = 1;
-  if (splits >= 2 && tiles <= kMaxCutTiles) {
+  if (is_tile256(pl.cfg)) {
+    pl.dp_tiles = splits == 1 ? tiles : (int)tile256_whole(tiles, cus);
+  } else if (splits >= 2 && tiles <= kMaxCutTiles) {
     pl.ksplit = std::min(splits, pl.stages);
     if (pl.ksplit >= 2) pl.dp_tiles = 0;
   } else if (splits == 0 && pl.stages >= 2) {
@@ -132,8 +165,9 @@ W4A16Plan plan_w4a16(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, i
     }
   }
   pl.grid = pl.dp_tiles + (tiles - pl.dp_tiles) * pl.ksplit;
-  const size_t partial_bytes =
-      pl.dp_tiles < tiles ? (size_t)(tiles - pl.dp_tiles) * pl.ksplit * pl.BM * pl.BN * sizeof(float) : 0;
+  const size_t partial_bytes = (pl.dp_tiles < tiles && !is_tile256(pl.cfg))
+                                   ? (size_t)(tiles - pl.dp_tiles) * pl.ksplit * pl.BM * pl.BN * sizeof(float)
+                                   : 0;
   pl.off_row_scale = 0;
   pl.off_x16 = pl.off_row_scale + (pl.prepass ? align256((size_t)M * sizeof(float)) : 0);
   pl.off_partial = pl.off_x16 + (pl.prepass ? align256((size_t)M * K * 2) : 0);
@@ -188,7 +222,18 @@ int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const float* r
                 out_dtype);
   if (int rc = check_w4a16_shape(M, N, K)) return rc;
   if (splits < 0 || splits > 64) return fail(QL_ERR_ARG, "splits must be in [0, 64], got %d", splits);
-  if (flags & ~QL_W4A16_BF16_MFMA) return fail(QL_ERR_ARG, "unknown flags 0x%x", flags);
+  if (flags & ~(QL_W4A16_BF16_MFMA | QL_W4A16_GELU_TANH | QL_W4A16_CFG_MASK))
+    return fail(QL_ERR_ARG, "unknown flags 0x%x", flags);
+  {
+    const int forced = (flags & QL_W4A16_CFG_MASK) >> QL_W4A16_CFG_SHIFT;
+    if (forced > kCfgLast + 1) return fail(QL_ERR_ARG, "flags: kernel configuration %d does not exist (0-%d)",
+                                           forced - 1, kCfgLast);
+    if (forced && is_tile256(forced - 1) && K % 64 != 0)
+      return fail(QL_ERR_SHAPE, "kernel configuration %d needs K %% 64 == 0, got K=%lld", forced - 1, (long long)K);
+    if (forced && is_tile256(forced - 1) && splits >= 2)
+      return fail(QL_ERR_ARG, "kernel configuration %d runs whole tiles only (splits 0 or 1), got splits=%d",
+                  forced - 1, splits);
+  }
   if (row_scale && x_dtype != QL_F16)
     return fail(QL_ERR_ARG, "row_scale is only accepted with float16 x (from qlinear_rows_to_f16), got %s",
                 dtype_name(x_dtype));
@@ -225,13 +270,16 @@ int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const float* r
   p.N = (int)N;
   p.K = (int)K;
   p.out_dtype = out_dtype;
+  p.act = (flags & QL_W4A16_GELU_TANH) ? kActGeluTanh : kActNone;
   p.tiles_m = pl.tiles_m;
   p.tiles_n = pl.tiles_n;
   p.stages = pl.stages;
   p.dp_tiles = pl.dp_tiles;
   p.ksplit = pl.ksplit;
   const bool bf16_mfma = x_dtype == QL_BF16 && !pl.prepass;
-  const hipError_t e = w4a16_launch(pl.cfg, bf16_mfma, p, (hipStream_t)stream);
+  const hipError_t e = is_tile256(pl.cfg)
+                           ? w4a16_tile256_launch(pl.cfg - kCfgTile256, bf16_mfma, p, (hipStream_t)stream)
+                           : w4a16_launch(pl.cfg, bf16_mfma, p, (hipStream_t)stream);
   if (e != hipSuccess) return fail(QL_ERR_LAUNCH, "w4a16 launch failed: %s", hipGetErrorString(e));
   return ok();
 }

@@ -59,6 +59,27 @@ __device__ __forceinline__ void write_elem(void* p, int dt, size_t i, float v) {
   }
 }
 
+// Round v to the 16-bit dtype dt (kBF16 / kF16, RNE) and back to fp32; fp32 passes through.
+__device__ __forceinline__ float round_to(int dt, float v) {
+  if (dt == kBF16) return (float)(__bf16)v;
+  if (dt == kF16) return (float)(_Float16)v;
+  return v;
+}
+
+// GELU, tanh approximation, in fp32: 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3), the
+// form of torch.nn.functional.gelu(approximate="tanh") that the reference's DiT MLP applies between
+// its two linears. Evaluated through the identity 0.5 (1 + tanh(u)) =
+// 1 / (1 + e^(-2u)): one exp2 and one reciprocal instead of a tanhf (about 30 instructions), so
+// the epilogue of a 4608 x 12288 output does not stall the GEMM. Relative error a few fp32 ulp,
+// below the rounding of a 16-bit output. x -> -inf gives 1 / inf = 0 and -0.0; x -> +inf gives x.
+__device__ __forceinline__ float gelu_tanh(float x) {
+  // -2 u log2(e) = x (c1 + c2 x^2)
+  const float c1 = -2.0f * 0.7978845608028654f * 1.4426950408889634f;
+  const float c2 = c1 * 0.044715f;
+  const float t = x * (c1 + c2 * (x * x));
+  return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t));
+}
+
 // ---- compile-time loops ----------------------------------------------------------------------
 // static_for<B, E>(f) calls f(std::integral_constant<int, i>{}) for i = B .. E-1 as straight-line
 // code: the index is a constant expression inside f, so register arrays indexed by it stay in

@@ -7,6 +7,8 @@
 
 namespace qlinear {
 
+enum Activation { kActNone = 0, kActGeluTanh = 1 };
+
 struct W4A16Params {
   const void* x;         // [M, K] bf16 / fp16
   const void* wq;        // [N, K/2] packed int4
@@ -17,10 +19,12 @@ struct W4A16Params {
   float* partial;        // partial tiles of the cut tiles: (tiles - dp_tiles) * ksplit slots of BM * BN fp32
   int M, N, K;
   int out_dtype;
+  int act;               // epilogue activation: kActNone or kActGeluTanh (256 x 256 kernel only)
   int tiles_m, tiles_n;
   int stages;            // K loop steps: ceil(K / (128 * w4a16_nbuf(WM)))
   int dp_tiles;          // tiles processed whole, one workgroup each
   int ksplit;            // K pieces of every tile past dp_tiles (>= 2 when any)
+  int tile_base;         // 256 x 256 kernel: first tile of the launch (set by the launcher)
 };
 
 struct W4A16Config {
@@ -35,6 +39,11 @@ int w4a16_steps(int cfg, int64_t K);
 
 const W4A16Config& w4a16_config(int id);
 hipError_t w4a16_launch(int cfg, bool bf16, const W4A16Params& p, hipStream_t stream);
+// 256 x 256 tiles, 32x32x16 MFMA (w4a16_tile256.hip), K % 64 == 0. Variant 0: 8 waves as 2 x 4
+// (128 x 64 each); 1: 8 waves as 1 x 8 (256 x 32); 2: 4 waves as 1 x 4 (256 x 64). The first
+// p.dp_tiles tiles (grouped order) run whole, the rest as two 128-row halves each (second launch).
+constexpr int kTile256Variants = 3;
+hipError_t w4a16_tile256_launch(int variant, bool bf16, const W4A16Params& p, hipStream_t stream);
 hipError_t rows_to_scaled_f16_launch(int dtype, const void* x, void* x16, float* row_scale, int64_t M,
                                      int64_t K, hipStream_t stream);
 

@@ -293,7 +293,7 @@ __global__ __launch_bounds__(64 * kWaves) void w4a16_gemm_kernel(W4A16Params p) 
   // A whole tile goes to y (row scale, bias, out dtype); a cut tile's piece goes as plain fp32 to
   // its partial slot, a tile-local [BM][BN] array. Same store loop for both.
   void* dst = p.y;
-  int dst_m0 = m0, dst_n0 = n0, dst_M = M, dst_N = N, dst_dtype = p.out_dtype;
+  int dst_m0 = m0, dst_n0 = n0, dst_M = M, dst_N = N, dst_dtype = p.out_dtype, dst_act = p.act;
   const void* bias = p.bias;
   const float* row_scale = p.row_scale;
   if constexpr (kCut) {
@@ -303,6 +303,7 @@ __global__ __launch_bounds__(64 * kWaves) void w4a16_gemm_kernel(W4A16Params p) 
     dst_M = BM;
     dst_N = BN;
     dst_dtype = kF32;
+    dst_act = kActNone;
     bias = nullptr;
     row_scale = nullptr;
   }
@@ -324,7 +325,10 @@ __global__ __launch_bounds__(64 * kWaves) void w4a16_gemm_kernel(W4A16Params p) 
         const int n = dst_n0 + (wn * WN + fn) * 16 + 4 * j4;
         float v[4];
 #pragma unroll
-        for (int e = 0; e < 4; ++e) v[e] = acc[fm][fn][e] * rs + bv[fn][e];
+        for (int e = 0; e < 4; ++e) {
+          v[e] = acc[fm][fn][e] * rs + bv[fn][e];
+          if (dst_act == kActGeluTanh) v[e] = gelu_tanh(round_to(dst_dtype, v[e]));
+        }
         const size_t off = (size_t)m * dst_N + n;
         if (vec && n + 3 < dst_N) {
           if (dst_dtype == kF32) {
@@ -373,7 +377,9 @@ __global__ __launch_bounds__(256) void w4a16_reduce_kernel(W4A16Params p, int BM
     const int n = tn * BN + idx % BN + e;
     if (n >= p.N) continue;
     const float bv = p.bias ? read_elem(p.bias, p.out_dtype, n) : 0.0f;
-    write_elem(p.y, p.out_dtype, (size_t)m * p.N + n, v[e] * rs + bv);
+    float out = v[e] * rs + bv;
+    if (p.act == kActGeluTanh) out = gelu_tanh(round_to(p.out_dtype, out));
+    write_elem(p.y, p.out_dtype, (size_t)m * p.N + n, out);
   }
 }
 

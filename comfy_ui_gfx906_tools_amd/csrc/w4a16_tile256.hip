@@ -1,0 +1,424 @@
+// W4A16 GEMM for large M on gfx950: y[M,N] = x[M,K] @ (q[N,K] * s[N,K/32])^T (+ bias), x fp16
+// (or bf16), q packed int4 in the reference layout (nodes/ComfyUI-Gfx906Int4/ops.py:108-126),
+// fp32 group scales, fp32 MFMA accumulation. Same arithmetic as w4a16_gemm.hip; a different
+// shape of workgroup, for M in the thousands.
+//
+// One 512-thread workgroup (8 waves, two per SIMD) computes a 256 x 256 output tile:
+//
+// * Waves sit 2 (along M) x 4 (along N); each owns 128 rows x 64 columns as 4 x 2 blocks of
+//   v_mfma_f32_32x32x16 (128 fp32 accumulators). Two waves per SIMD let one wave's dequant run
+//   on the VALU while the other's MFMAs run on the matrix core.
+// * Everything a stage needs arrives by DMA straight into LDS (buffer_load ... lds), 64 K per
+//   stage: activations (256 rows x 128 B), raw int4 weights (256 columns x 32 B) and the group
+//   scales (256 columns x 2 x 4 B), 42 KiB per stage, three stage buffers; the loads of stage
+//   s+2 are issued during stage s.
+// * The weights are the MFMA's first operand (rows of the 32x32 block = output columns n), the
+//   activations its second (block columns = rows m of y). Lane (c = l % 32, h = l / 32) of a
+//   weight fragment holds column c and quant group h of the stage: one 16-byte read from LDS
+//   gives the lane the 32 nibbles of its group; K-step t of the stage dequantizes dword t (8
+//   weights) in registers. The K-slot map of an MFMA is therefore: slot block h of K-step t =
+//   K elements 32h + 8t .. +7 of the stage, and the activation fragment is read with the same
+//   map (row m, 16-byte chunk 4h + t).
+// * LDS swizzles (swz_a, swz_b) make every 16-byte operand read conflict free: activation rows
+//   are 128 B, weight columns 32 B.
+// * Rows past M, columns past N read zeros (buffer range checks); K must be a multiple of 64.
+// * Epilogue: lane (m, h) of an accumulator block holds y[m][n .. n+3] for n = 8b + 4h, b = 0..3
+//   (the transpose of the MFMA's row-major output): bias, optional exact row scale, rounding to
+//   the output dtype, one 8- or 16-byte store per 4 outputs.
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace qlinear {
+
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+constexpr int kT256StageK = 64;
+constexpr int kT256NBuf = 3;
+constexpr int kT256GroupM = 4;
+
+template <bool kBf16>
+__device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {
+  if constexpr (kBf16) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8, a), __builtin_bit_cast(bf16x8, b), c, 0,
+                                                  0, 0);
+  } else {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c, 0, 0,
+                                                 0);
+  }
+}
+
+// 4-byte DMA (buffer_load_dword ... lds): lane i writes lds_base + 4 * i.
+__device__ __forceinline__ void buf_load4_lds(rsrc_t r, void* lds_base, uint32_t voff, uint32_t soff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(r, (__attribute__((address_space(3))) void*)lds_base, 4, voff, soff, 0, 0);
+}
+
+// LDS swizzles. A 16-byte operand read (ds_read_b128) is served 16 lanes (256 B) or 32 lanes
+// (512 B) at a time; both are conflict free when the lanes of a pass hit distinct 16-byte slots
+// of the 256- or 512-byte window. Activation reads take rows r .. r+31 (lanes 0-31) at one logical
+// chunk: with 128-byte rows, rows of equal r & 1 (256-byte pass) and of equal r & 3 (512-byte
+// pass) must use distinct physical chunks, which needs bits 1-3 and bits 2-4 of r to each map
+// one-to-one onto the chunk: chunk ^ (bits 1-3 of r) ^ (bit 4 of r). Weight reads take columns
+// n .. n+31 at one half: columns n and n + 8 (256-byte pass) and n and n + 16 (512-byte pass)
+// must use different halves: half ^ bit 3 ^ bit 4 of n.
+__device__ __forceinline__ int swz_a(int r) { return ((r >> 1) & 7) ^ ((r >> 4) & 1); }
+__device__ __forceinline__ int swz_b(int n) { return ((n >> 3) & 1) ^ ((n >> 4) & 1); }
+
+// Waves sit kWavesM (along M) x kWavesN (along N); each owns (32 WM) rows x (32 WN) columns as
+// WM x WN blocks of v_mfma_f32_32x32x16. The tile is BM = 32 WM kWavesM rows by
+// BN = 32 WN kWavesN columns.
+// A workgroup computes sub-tile (g % kSub) along M of the 256 x 256 tile p.tile_base + g / kSub
+// (grouped tile order): kSub = 1 for whole tiles, 2 for the 128-row halves that the last,
+// partly filled round of tiles is cut into.
+template <bool kBf16, int kWavesM, int kWavesN, int WM, int WN, int kSub>
+__global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W4A16Params p) {
+  constexpr int kWaves = kWavesM * kWavesN;
+  constexpr int BM = 32 * WM * kWavesM, BN = 32 * WN * kWavesN;
+  constexpr int kABytes = BM * kT256StageK * 2;  // activations: BM rows x 128 B
+  constexpr int kBBytes = BN * kT256StageK / 2;  // weights: BN columns x 32 B
+  constexpr int kSBytes = BN * 2 * 4;            // scales: BN columns x 2 groups x 4 B
+  constexpr int kStageBytes = kABytes + kBBytes + kSBytes;
+  // DMA instructions per wave and stage: activations in 1 KiB blocks (8 rows), weights in 1 KiB
+  // blocks (32 columns), scales in 256 B blocks (32 columns)
+  constexpr int nA = BM / 8 / kWaves, nB = BN / 32 / kWaves, nS = BN / 32 / kWaves;
+  constexpr int nL = nA + nB + nS;
+  static_assert(nA * 8 * kWaves == BM && nB * 32 * kWaves == BN && nB >= 1, "DMA blocks must split evenly");
+  static_assert(nL <= 4 * WM * WN, "the loads of a stage are spread over the MFMAs of a stage");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kT256NBuf * kStageBytes];
+
+  const int lane = threadIdx.x & 63;
+  const int w = threadIdx.x >> 6;
+  const int wm = w / kWavesN, wn = w % kWavesN;
+  const int c32 = lane & 31, h = lane >> 5;
+  const int M = p.M, N = p.N, K = p.K;
+  const int S = K / kT256StageK;
+
+  static_assert(BM * kSub == 256 && BN == 256, "sub-tiles of a 256 x 256 tile");
+  const int g = xcd_remap(blockIdx.x, gridDim.x);
+  int tm, tn;
+  tile_coords(p.tile_base + g / kSub, p.tiles_m, p.tiles_n, kT256GroupM, tm, tn);
+  const int m0 = tm * 256 + (g % kSub) * BM, n0 = tn * BN;
+  const int rows = min(M - m0, BM), cols = min(N - n0, BN);
+
+  const rsrc_t rs_a = make_rsrc((const uint16_t*)p.x + (size_t)m0 * K, (uint32_t)rows * K * 2);
+  const rsrc_t rs_b = make_rsrc((const uint8_t*)p.wq + (size_t)n0 * (K / 2), (uint32_t)cols * (K / 2));
+  const rsrc_t rs_s = make_rsrc(p.ws + (size_t)n0 * (K / 32), (uint32_t)cols * (K / 32) * 4);
+  const rsrc_t rs_none = make_rsrc(p.ws, 0);
+
+  // ---- DMA lane offsets (fixed for the K loop; the stage goes into the scalar offset) --------
+  // activation block kb = w nA + q: rows 8kb .. 8kb+7; lane i: row 8kb + i/8, physical chunk i%8
+  //   holding logical chunk (i%8) ^ swz_a(row)
+  uint32_t vo_a[nA];
+#pragma unroll
+  for (int q = 0; q < nA; ++q) {
+    const int r = 8 * (w * nA + q) + (lane >> 3);
+    vo_a[q] = (uint32_t)(r * K + 8 * ((lane & 7) ^ swz_a(r))) * 2;
+  }
+  // weight block kb = w nB + q: columns 32kb .. 32kb+31; lane i: column 32kb + i/2, physical half
+  //   i%2 holding group (i%2) ^ swz_b(column). Scale block likewise, lane i: group i%2.
+  uint32_t vo_b[nB], vo_s[nS];
+#pragma unroll
+  for (int q = 0; q < nB; ++q) {
+    const int n = 32 * (w * nB + q) + (lane >> 1);
+    vo_b[q] = (uint32_t)n * (K / 2) + 16 * ((lane & 1) ^ swz_b(n));
+    vo_s[q] = ((uint32_t)n * (K / 32) + (lane & 1)) * 4;
+  }
+
+  // DMA instruction l (0 .. nL-1) of this wave's share of stage s into ring buffer `buf`. A stage
+  // past the end loads through an empty resource (no traffic, no branch).
+  auto load_one = [&](int l, int s, int buf) {
+    uint8_t* base = lds + buf * kStageBytes;
+    const bool live = s < S;
+    if (l < nA) {
+      buf_load16_lds(live ? rs_a : rs_none, base + (w * nA + l) * 1024, vo_a[l], s * 128);
+    } else if (l < nA + nB) {
+      const int q = l - nA;
+      buf_load16_lds(live ? rs_b : rs_none, base + kABytes + (w * nB + q) * 1024, vo_b[q], s * 32);
+    } else {
+      const int q = l - nA - nB;
+      buf_load4_lds(live ? rs_s : rs_none, base + kABytes + kBBytes + (w * nS + q) * 256, vo_s[q], s * 8);
+    }
+  };
+  auto load_stage = [&](int s, int buf) {
+#pragma unroll
+    for (int l = 0; l < nL; ++l) load_one(l, s, buf);
+  };
+
+  // ---- LDS read addresses ------------------------------------------------------------------
+  // activation fragment (m-block j, K-step t): row wm*32*WM + 32j + c32, logical chunk 4h + t.
+  // The swizzle depends only on bits 1-4 of the row, those of c32, so one base per K-step serves
+  // every m-block (+ j * 4 KiB).
+  typedef __attribute__((address_space(3))) const u32x4* lds_frag_ptr;
+  const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds;
+  uint32_t a_off[4];
+#pragma unroll
+  for (int t = 0; t < 4; ++t) {
+    const int r = wm * 32 * WM + c32;
+    a_off[t] = (uint32_t)(r * 128 + (((4 * h + t) ^ swz_a(r)) * 16));
+  }
+  // weight fragment (n-block i): column wn*32*WN + 32i + c32, group h of the stage
+  uint32_t b_off[WN], s_off[WN];
+#pragma unroll
+  for (int i = 0; i < WN; ++i) {
+    const int n = wn * 32 * WN + 32 * i + c32;
+    b_off[i] = (uint32_t)(kABytes + n * 32 + 16 * (h ^ swz_b(n)));
+    s_off[i] = (uint32_t)(kABytes + kBBytes + n * 8 + 4 * h);
+  }
+  auto read_a = [&](int buf, int t, int j) {
+    return *(lds_frag_ptr)(lds_base + buf * kStageBytes + a_off[t] + j * 4096);
+  };
+  auto read_b = [&](int buf, int i) { return *(lds_frag_ptr)(lds_base + buf * kStageBytes + b_off[i]); };
+  auto read_s = [&](int buf, int i) {
+    return *(__attribute__((address_space(3))) const float*)(lds_base + buf * kStageBytes + s_off[i]);
+  };
+
+  // Accumulators start as the result of an MFMA on zeros rather than as a zero constant, which
+  // keeps the compiler from copying them between register files at every loop iteration.
+  f32x16 acc[WN][WM];
+  {
+    f32x16 z;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) z[e] = 0.0f;
+#pragma unroll
+    for (int i = 0; i < WN; ++i)
+#pragma unroll
+      for (int j = 0; j < WM; ++j) acc[i][j] = mfma32<kBf16>(u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}, z);
+  }
+
+  // ---- main loop ----------------------------------------------------------------------------
+  // Stage s sits in ring buffer s % 3. Entering stage s: its raw weights, scales and the
+  // activation fragments of K-step 0 are in registers (reads issued), the loads of stage s+1
+  // are in flight, and buffer (s+2) % 3 = (s-1) % 3 is free (every wave passed the barrier at the
+  // end of stage s-1). During stage s each wave issues its loads of stage s+2 into that buffer,
+  // spread evenly over the stage's MFMAs: issued in a burst, the DMA instructions of all waves
+  // fill the texture unit's address FIFO and stall the MFMAs queued behind them. Before the
+  // stage's last K-step every wave waits for its own loads of s+1 and passes the barrier (after
+  // which stage s+1 is complete in LDS and nobody reads buffer s % 3 any more); the last
+  // K-step's MFMAs then cover the reads of s+1's first fragments.
+  // Each activation fragment register is refilled in place with the fragment of the next K-step
+  // (of the next stage after the last K-step) right after its last MFMA of this K-step, so the
+  // reads have the rest of the K-step's MFMAs to land and only one set of fragments is live.
+  constexpr int kSlots = 4 * WM * WN;  // MFMAs per wave and stage
+  // DMA instruction l of stage s+2 goes after MFMA slot l * kSlots / nL of stage s; the ones before
+  // the last K-step (slot < 3 WM WN) are issued before that K-step's wait, which must let exactly
+  // those stay outstanding (vmcnt counts this wave's loads in issue order)
+  constexpr int kPreWait = [] {
+    int c = 0;
+    for (int l = 0; l < nL; ++l) c += (l * kSlots / nL < 3 * WM * WN) ? 1 : 0;
+    return c;
+  }();
+  u32x4 raw[WN], a[WM], b[WN], bn[WN];
+  float sc[WN];
+  auto first_weights = [&](auto bc) {
+    constexpr int bf = decltype(bc)::value;
+#pragma unroll
+    for (int i = 0; i < WN; ++i) {
+      raw[i] = read_b(bf, i);
+      sc[i] = read_s(bf, i);
+    }
+  };
+  auto stage = [&](auto bc, int s) {
+    constexpr int bf = decltype(bc)::value;
+    constexpr int bf1 = (bf + 1) % kT256NBuf, bf2 = (bf + 2) % kT256NBuf;
+    float n8s[WN];
+#pragma unroll
+    for (int i = 0; i < WN; ++i) {
+      n8s[i] = -8.0f * sc[i];
+      bn[i] = dequant8<kBf16>(raw[i][0], sc[i], n8s[i]);
+    }
+    static_for<0, 4>([&](auto tc) {
+      constexpr int t = decltype(tc)::value;
+#pragma unroll
+      for (int i = 0; i < WN; ++i) b[i] = bn[i];
+      if constexpr (t == 3) {
+        // this wave's reads of buffer bf are complete (the last ones fill a[] for this K-step)
+        // and its loads of stage s+1 have landed; after the barrier every wave's have
+        wait_lgkm();
+        wait_vmcnt<kPreWait>();
+        barrier_no_fence();
+        first_weights(ic<bf1>{});
+      }
+      static_for<0, WM>([&](auto jc) {
+        constexpr int j = decltype(jc)::value;
+        static_for<0, WN>([&](auto ic_) {
+          constexpr int i = decltype(ic_)::value;
+          constexpr int slot = (t * WM + j) * WN + i;
+          acc[i][j] = mfma32<kBf16>(b[i], a[j], acc[i][j]);
+          static_for<0, nL>([&](auto lc) {
+            constexpr int l = decltype(lc)::value;
+            if constexpr (l * kSlots / nL == slot) {
+              load_one(l, s + 2, bf2);
+              __builtin_amdgcn_sched_barrier(0);
+            }
+          });
+        });
+        a[j] = t < 3 ? read_a(bf, t + 1, j) : read_a(bf1, 0, j);
+        if constexpr (t < 3 && j < WN) bn[j] = dequant8<kBf16>(raw[j][t + 1], sc[j], n8s[j]);
+      });
+      __builtin_amdgcn_sched_barrier(0);
+    });
+  };
+
+  // ---- prologue: stages 0 and 1 in flight, stage 0 published --------------------------------
+  load_stage(0, 0);
+  load_stage(1, 1);
+  wait_vmcnt<nL>();
+  barrier_no_fence();
+  first_weights(ic<0>{});
+#pragma unroll
+  for (int j = 0; j < WM; ++j) a[j] = read_a(0, 0, j);
+
+  int s = 0;
+  for (; s + 3 <= S; s += 3) {
+    stage(ic<0>{}, s);
+    stage(ic<1>{}, s + 1);
+    stage(ic<2>{}, s + 2);
+  }
+  if (s < S) stage(ic<0>{}, s++);
+  if (s < S) stage(ic<1>{}, s++);
+
+  // ---- epilogue ----------------------------------------------------------------------------
+  // v = acc * row_scale + bias; with the GELU epilogue v is first rounded to the output dtype
+  // (the unfused sequence's linear output) and then passed through gelu_tanh. Bias and row
+  // scales go to registers before any store (y may alias them as far as the compiler knows).
+  // (The pointers pass through an empty asm statement so the loads are not hoisted above the K
+  // loop, where their registers would be live across it.)
+  const void* bias_p = p.bias;
+  const float* rs_p = p.row_scale;
+  asm volatile("" : "+s"(bias_p), "+s"(rs_p));
+  float bv[WN][4][4], rsj[WM];
+#pragma unroll
+  for (int i = 0; i < WN; ++i)
+#pragma unroll
+    for (int bq = 0; bq < 4; ++bq)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int n = n0 + wn * 32 * WN + 32 * i + 8 * bq + 4 * h + e;
+        bv[i][bq][e] = (bias_p && n < N) ? read_elem(bias_p, p.out_dtype, n) : 0.0f;
+      }
+#pragma unroll
+  for (int j = 0; j < WM; ++j) {
+    const int m = m0 + wm * 32 * WM + 32 * j + c32;
+    rsj[j] = (rs_p && m < M) ? rs_p[m] : 1.0f;
+  }
+  const int act = p.act, odt = p.out_dtype;
+  auto value = [&](int i, int j, int bq, int e) {
+    float v = acc[i][j][4 * bq + e] * rsj[j] + bv[i][bq][e];
+    if (act == kActGeluTanh) v = gelu_tanh(round_to(odt, v));
+    return v;
+  };
+
+  if (odt == kF32) {
+    // fp32: lane (m, h) stores 4 adjacent outputs (16 B) per accumulator quarter
+    const bool vec = (N % 4) == 0 && (((uintptr_t)p.y) & 15) == 0;
+#pragma unroll
+    for (int j = 0; j < WM; ++j) {
+      const int m = m0 + wm * 32 * WM + 32 * j + c32;
+      if (m >= M) continue;
+#pragma unroll
+      for (int i = 0; i < WN; ++i)
+#pragma unroll
+        for (int bq = 0; bq < 4; ++bq) {
+          const int n = n0 + wn * 32 * WN + 32 * i + 8 * bq + 4 * h;
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) v[e] = value(i, j, bq, e);
+          const size_t off = (size_t)m * N + n;
+          if (vec && n + 3 < N) {
+            *(f32x4*)((float*)p.y + off) = f32x4{v[0], v[1], v[2], v[3]};
+          } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (n + e < N) ((float*)p.y)[off + e] = v[e];
+          }
+        }
+    }
+    return;
+  }
+
+  // 16-bit outputs go through LDS, half a tile (BM/2 rows x BN columns, 64 KiB) at a time, so that
+  // each wave stores whole 512-byte row segments with 16-byte lanes instead of 8-byte pieces of
+  // 32 different rows. LDS row r holds 16-byte chunk c at slot c ^ (r & 31): the 8-byte writes of
+  // a wave (32 rows x 2 halves of one chunk) and the 16-byte reads (2 rows x 32 chunks) are both
+  // conflict free. The stage buffers are free once every wave is past its last MFMA and the DMA
+  // loads issued for stages past the end (which write zeros) have landed.
+  constexpr int kHalfRows = BM / 2;
+  constexpr int kChunks = BN / 8;  // 16-byte chunks per row
+  static_assert(kHalfRows * BN * 2 <= kT256NBuf * kStageBytes, "half a tile must fit the stage buffers");
+  wait_vmcnt<0>();
+  wait_lgkm();
+  barrier_no_fence();
+  const bool bf_out = odt == kBF16;
+  const bool vec = (N % 8) == 0 && (((uintptr_t)p.y) & 15) == 0;
+  static_for<0, 2>([&](auto hc) {
+    constexpr int half = decltype(hc)::value;
+#pragma unroll
+    for (int j = 0; j < WM; ++j) {
+      const int rt = wm * 32 * WM + 32 * j;  // first tile row of block j
+      if (rt / kHalfRows != half) continue;
+      const int r = rt - half * kHalfRows + c32;
+#pragma unroll
+      for (int i = 0; i < WN; ++i)
+#pragma unroll
+        for (int bq = 0; bq < 4; ++bq) {
+          const int c = wn * 32 * WN + 32 * i + 8 * bq + 4 * h;  // tile column of the lane's 4 outputs
+          const uint32_t lo = bf_out ? pack2_bf16(value(i, j, bq, 0), value(i, j, bq, 1))
+                                     : pack2_f16(value(i, j, bq, 0), value(i, j, bq, 1));
+          const uint32_t hi = bf_out ? pack2_bf16(value(i, j, bq, 2), value(i, j, bq, 3))
+                                     : pack2_f16(value(i, j, bq, 2), value(i, j, bq, 3));
+          typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+          *(u32x2*)(lds + r * (BN * 2) + (((c >> 3) ^ (r & 31)) << 4) + (c & 7) * 2) = u32x2{lo, hi};
+        }
+    }
+    barrier_no_fence();
+    for (int q = threadIdx.x; q < kHalfRows * kChunks; q += 64 * kWaves) {
+      const int r = q / kChunks, c = q % kChunks;
+      const u32x4 v = *(const u32x4*)(lds + r * (BN * 2) + ((c ^ (r & 31)) << 4));
+      const int m = m0 + half * kHalfRows + r, n = n0 + 8 * c;
+      if (m >= M || n >= N) continue;
+      uint16_t* dst = (uint16_t*)p.y + (size_t)m * N + n;
+      if (vec && n + 8 <= N) {
+        *(u32x4*)dst = v;
+      } else {
+        for (int e = 0; e < 8 && n + e < N; ++e) dst[e] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
+      }
+    }
+    if constexpr (half == 0) barrier_no_fence();
+  });
+}
+
+template <bool kBf16, int kWavesM, int kWavesN, int WM, int WN>
+hipError_t launch_variant(const W4A16Params& p, hipStream_t stream) {
+  W4A16Params q = p;
+  const int tiles = p.tiles_m * p.tiles_n;
+  const int whole = p.dp_tiles;  // tiles run whole; the rest as 128-row halves
+  if (whole > 0) {
+    q.tile_base = 0;
+    hipLaunchKernelGGL((w4a16_tile256_kernel<kBf16, kWavesM, kWavesN, WM, WN, 1>), dim3(whole),
+                       dim3(64 * kWavesM * kWavesN), 0, stream, q);
+  }
+  if (whole < tiles) {
+    q.tile_base = whole;
+    hipLaunchKernelGGL((w4a16_tile256_kernel<kBf16, 1, 8, 4, 1, 2>), dim3(2 * (tiles - whole)), dim3(512), 0, stream,
+                       q);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t w4a16_tile256_launch(int variant, bool bf16, const W4A16Params& p, hipStream_t stream) {
+  switch (variant) {
+    case 0:  // 8 waves, 2 x 4, each 128 x 64
+      return bf16 ? launch_variant<true, 2, 4, 4, 2>(p, stream) : launch_variant<false, 2, 4, 4, 2>(p, stream);
+    case 1:  // 8 waves, 1 x 8, each 256 x 32
+      return bf16 ? launch_variant<true, 1, 8, 8, 1>(p, stream) : launch_variant<false, 1, 8, 8, 1>(p, stream);
+    case 2:  // 4 waves, 1 x 4, each 256 x 64
+      return bf16 ? launch_variant<true, 1, 4, 8, 2>(p, stream) : launch_variant<false, 1, 4, 8, 2>(p, stream);
+    default:
+      return hipErrorInvalidValue;
+  }
+}
+
+}  // namespace qlinear

@@ -71,6 +71,18 @@ int qlinear_abi_version(void);
  *             needed. Calls sharing one workspace must be ordered (same stream).
  * ------------------------------------------------------------------------------------- */
 #define QL_W4A16_BF16_MFMA 1 /* flags bit, see above */
+/* flags bit: GELU (tanh approximation) epilogue, y = gelu(round(x @ W^T + bias)) with the linear's
+ * result first rounded to out_dtype, then gelu_tanh in fp32 and rounded again -- the sequence
+ * Linear -> nn.GELU(approximate="tanh") of the DiT MLP, in one kernel (no counterpart in the
+ * reference's extension, whose GELU is a separate torch op). */
+#define QL_W4A16_GELU_TANH 2
+/* flags bits 8-11: 0 = automatic kernel choice, c + 1 = force kernel configuration c
+ * (0-3: 256 / 128 / 64 / 16-row x 256-column tiles, 4 waves; 4-6: 256 x 256 tiles with 8 waves
+ * as 2 x 4, 8 waves as 1 x 8, 4 waves as 1 x 4, K % 64 == 0, whole tiles only). For tuning and
+ * tests; results agree to rounding. */
+#define QL_W4A16_CFG_SHIFT 8
+#define QL_W4A16_CFG_MASK (0xF << QL_W4A16_CFG_SHIFT)
+#define QL_W4A16_CFG(c) (((c) + 1) << QL_W4A16_CFG_SHIFT)
 
 size_t qlinear_w4a16_workspace_bytes(int x_dtype, int64_t M, int64_t N, int64_t K, int splits,
                                      int flags, int device);

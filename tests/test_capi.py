@@ -89,6 +89,18 @@ def test_w4a16_argument_checks(lib):
     assert "null" in _err(lib)
     assert f(1, 2, ctypes.c_void_p(8), None, ctypes.c_void_p(16), ctypes.c_void_p(16), None, ctypes.c_void_p(16),
              4, 64, 64, 0, 0, None, 0, None) == QL_ERR_ALIGN
+    # forced kernel configurations (flags bits 8-11 = configuration + 1): 0-6 exist; the 256 x 256
+    # configurations 4-6 need K % 64 == 0 and whole tiles
+    cfg = lambda c: (c + 1) << 8  # noqa: E731
+    assert f(2, 2, None, None, None, None, None, None, 0, 64, 64, 0, cfg(7), None, 0, None) == QL_ERR_ARG
+    assert "configuration 7 does not exist" in _err(lib)
+    for c in range(7):
+        assert f(2, 2, None, None, None, None, None, None, 0, 64, 64, 0, cfg(c), None, 0, None) == QL_OK
+    for c in (4, 5, 6):
+        assert f(2, 2, None, None, None, None, None, None, 0, 64, 96, 0, cfg(c), None, 0, None) == QL_ERR_SHAPE
+        assert "K % 64 == 0" in _err(lib)
+        assert f(2, 2, None, None, None, None, None, None, 0, 64, 128, 2, cfg(c), None, 0, None) == QL_ERR_ARG
+        assert "whole tiles" in _err(lib)
 
 
 def test_quantizer_and_w8a8_argument_checks(lib):

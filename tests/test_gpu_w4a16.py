@@ -155,3 +155,111 @@ def test_w4a16_baseline_shapes_vs_torch_fp32(M, K, N, xdt):
     err = ((y - ref).abs().max() / ref.abs().max()).item()
     del w
     assert err <= TOL, f"max rel err {err:.3e}"
+
+
+# Every kernel configuration, forced through the flags field (QL_W4A16_CFG): 0-3 are the
+# 4-wave kernel's 256/128/64/16-row tiles, 4-6 the 256 x 256 kernel's wave layouts.
+ALL_CFGS = list(range(7))
+TILE256_CFGS = [4, 5, 6]
+
+
+def _run_cfg(x, wq, ws, bias=None, out_dtype=torch.float32, cfg=None, bf16_mfma=False):
+    return _lib().w4a16_gemm(x.to(DEV), wq.to(DEV), ws.to(DEV), None if bias is None else bias.to(DEV),
+                             out_dtype=out_dtype, bf16_mfma=bf16_mfma, config=cfg)
+
+
+@pytest.mark.parametrize("cfg", ALL_CFGS)
+@pytest.mark.parametrize("M,N,K,xdt", [(300, 200, 192, torch.bfloat16), (513, 777, 640, torch.float16),
+                                       (256, 512, 3072, torch.bfloat16)])
+def test_w4a16_every_config_vs_oracle(cfg, M, N, K, xdt):
+    """Ragged M and N (tiles past the edges), bias, fp32 out: each configuration within the gate,
+    and two runs bit-identical."""
+    print(f"case cfg={cfg} M={M} N={N} K={K} x={xdt}", flush=True)
+    x, wq, ws = seeded_linear(M, N, K, seed=M + 3 * N + K + cfg, x_dtype=xdt)
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(cfg))
+    y1 = _run_cfg(x, wq, ws, bias, cfg=cfg)
+    y2 = _run_cfg(x, wq, ws, bias, cfg=cfg)
+    assert torch.equal(y1, y2), "not deterministic"
+    ref = orc.w4a16_reference(to_np_f32(x), wq.numpy(), ws.numpy(), bias.numpy())
+    err = rel_max_err(to_np_f32(y1), ref)
+    assert err <= TOL, f"cfg {cfg}: max rel err {err:.3e} > {TOL}"
+
+
+@pytest.mark.parametrize("cfg", ALL_CFGS)
+def test_w4a16_every_config_exact_on_integer_grid(cfg):
+    """The exact-grid case of test_w4a16_exact_on_integer_grid through each configuration."""
+    M, N, K = 290, 300, 256
+    print(f"case exact grid cfg={cfg}", flush=True)
+    g = np.random.default_rng(19 + cfg)
+    x = torch.from_numpy(g.integers(-4, 5, (M, K)).astype(np.float32)).to(torch.bfloat16)
+    codes = g.integers(-8, 8, (N, K))
+    nib = (codes & 0xF).astype(np.uint8)
+    packed = (nib[:, 0::2] | (nib[:, 1::2] << 4)).view(np.int8)
+    scale = (2.0 ** g.integers(-6, 0, (N, K // 32))).astype(np.float32)
+    y = to_np_f32(_run_cfg(x, torch.from_numpy(packed), torch.from_numpy(scale), cfg=cfg))
+    ref = orc.w4a16_reference(to_np_f32(x), packed, scale)
+    assert np.array_equal(y.astype(np.float64), ref), f"cfg {cfg}: max abs diff {np.abs(y - ref).max()}"
+
+
+@pytest.mark.parametrize("cfg", TILE256_CFGS)
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16])
+def test_w4a16_tile256_bf16_mfma_and_16bit_out(cfg, out_dtype):
+    """bf16 MFMA mode (tight gate against the reference's bf16 dequant-then-matmul) and 16-bit
+    outputs with bias (1 ulp + gate) on the 256 x 256 kernel."""
+    M, N, K = 300, 520, 1024
+    print(f"case tile256 cfg={cfg} out={out_dtype}", flush=True)
+    x, wq, ws = seeded_linear(M, N, K, seed=23 + cfg)
+    y = to_np_f32(_run_cfg(x, wq, ws, cfg=cfg, bf16_mfma=True))
+    w_bf16 = orc.round_to_bf16(orc.dequant_int4(wq.numpy(), ws.numpy())).astype(np.float64)
+    assert rel_max_err(y, to_np_f32(x).astype(np.float64) @ w_bf16.T) <= 2e-5
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(4)).to(out_dtype)
+    y = to_np_f32(_run_cfg(x, wq, ws, bias, out_dtype=out_dtype, cfg=cfg))
+    ref = orc.w4a16_reference(to_np_f32(x), wq.numpy(), ws.numpy(), to_np_f32(bias)).astype(np.float32)
+    name = "bfloat16" if out_dtype == torch.bfloat16 else "float16"
+    ref_r = orc.round_to_dtype(ref, name)
+    ulp = bf16_ulp(ref_r) if out_dtype == torch.bfloat16 else f16_ulp(ref_r)
+    bound = ulp + TOL * np.abs(ref).max()
+    assert (np.abs(y - ref_r) <= bound).all(), f"max excess {(np.abs(y - ref_r) - bound).max():.3e}"
+
+
+@pytest.mark.parametrize("cfg", TILE256_CFGS)
+def test_w4a16_tile256_rejects_k_not_multiple_of_64(cfg):
+    x, wq, ws = seeded_linear(64, 256, 96, seed=1)
+    with pytest.raises(RuntimeError, match="K % 64"):
+        _run_cfg(x, wq, ws, cfg=cfg)
+
+
+def _gelu_tanh_f64(v: np.ndarray) -> np.ndarray:
+    """GELU, tanh approximation, in float64 (the formula of torch.nn.functional.gelu(approximate="tanh"))."""
+    v = v.astype(np.float64)
+    return 0.5 * v * (1.0 + np.tanh(np.sqrt(2.0 / np.pi) * (v + 0.044715 * v ** 3)))
+
+
+@pytest.mark.parametrize("cfg", [None, 1, 3, 5])
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float32])
+def test_w4a16_fused_gelu_matches_unfused(cfg, out_dtype):
+    """QL_W4A16_GELU_TANH: gelu_tanh(round(y)) in the epilogue. `plain` is the same kernel's output
+    without the epilogue (the linear rounded to out_dtype); the fused result must equal the float64
+    GELU of `plain`, rounded to out_dtype, within 1 ulp (16-bit) or 1e-5 relative + 1e-6 absolute
+    (fp32: the epilogue evaluates 0.5 (1 + tanh(u)) as 1 / (1 + exp(-2u)) with the hardware exp2 and
+    reciprocal). torch's unfused gelu on `plain` is also checked, within 2 ulp + 1e-6 absolute: its
+    0.5 x (1 + tanh(u)) cancels in the negative tail (absolute error ~1e-7 there). M = 300 with cfg None takes the automatic plan,
+    including K-cut tiles and their reduction for the 4-wave kernel."""
+    M, N, K = (300, 1040, 1024) if cfg != 3 else (9, 700, 512)
+    print(f"case gelu cfg={cfg} out={out_dtype}", flush=True)
+    x, wq, ws = seeded_linear(M, N, K, seed=31, x_dtype=torch.bfloat16)
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(5)).to(out_dtype)
+    plain = _run_cfg(x, wq, ws, bias, out_dtype=out_dtype, cfg=cfg)
+    fused = _lib().w4a16_gemm(x.to(DEV), wq.to(DEV), ws.to(DEV), bias.to(DEV), out_dtype=out_dtype, config=cfg,
+                              gelu=True)
+    f = to_np_f32(fused)
+    exact = _gelu_tanh_f64(to_np_f32(plain))
+    r_torch = to_np_f32(torch.nn.functional.gelu(plain, approximate="tanh"))
+    if out_dtype == torch.bfloat16:
+        e = orc.round_to_dtype(exact.astype(np.float32), "bfloat16")
+        ulp = bf16_ulp(e)
+        assert (np.abs(f - e) <= ulp).all(), f"max diff vs exact {np.abs(f - e).max():.3e}"
+        assert (np.abs(f - r_torch) <= 2 * bf16_ulp(r_torch) + 1e-6).all()
+    else:
+        assert (np.abs(f - exact) <= 1e-5 * np.abs(exact) + 1e-6).all(), f"max diff {np.abs(f - exact).max():.3e}"
+        assert (np.abs(f - r_torch) <= 1e-5 * np.abs(r_torch) + 1e-6).all()
