@@ -88,7 +88,9 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W
   __shared__ __attribute__((aligned(1024))) uint8_t lds[kT256NBuf * kStageBytes];
 
   const int lane = threadIdx.x & 63;
-  const int w = threadIdx.x >> 6;
+  // the wave index is uniform across the wave: in a scalar register, LDS destinations of the DMA
+  // (M0) and other per-wave values are computed with scalar instructions
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int wm = w / kWavesN, wn = w % kWavesN;
   const int c32 = lane & 31, h = lane >> 5;
   const int M = p.M, N = p.N, K = p.K;
@@ -125,19 +127,22 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W
     vo_s[q] = ((uint32_t)n * (K / 32) + (lane & 1)) * 4;
   }
 
+  // LDS layout: the three activation stage buffers, then the three weight buffers, then the three
+  // scale buffers, so that every operand read of buffers 0 and 1 (and the weight and scale reads of
+  // all three) fits the 16-bit immediate offset of ds_read from one base register.
+  constexpr int kOffB = kT256NBuf * kABytes, kOffS = kOffB + kT256NBuf * kBBytes;
   // DMA instruction l (0 .. nL-1) of this wave's share of stage s into ring buffer `buf`. A stage
   // past the end loads through an empty resource (no traffic, no branch).
   auto load_one = [&](int l, int s, int buf) {
-    uint8_t* base = lds + buf * kStageBytes;
     const bool live = s < S;
     if (l < nA) {
-      buf_load16_lds(live ? rs_a : rs_none, base + (w * nA + l) * 1024, vo_a[l], s * 128);
+      buf_load16_lds(live ? rs_a : rs_none, lds + buf * kABytes + (w * nA + l) * 1024, vo_a[l], s * 128);
     } else if (l < nA + nB) {
       const int q = l - nA;
-      buf_load16_lds(live ? rs_b : rs_none, base + kABytes + (w * nB + q) * 1024, vo_b[q], s * 32);
+      buf_load16_lds(live ? rs_b : rs_none, lds + kOffB + buf * kBBytes + (w * nB + q) * 1024, vo_b[q], s * 32);
     } else {
       const int q = l - nA - nB;
-      buf_load4_lds(live ? rs_s : rs_none, base + kABytes + kBBytes + (w * nS + q) * 256, vo_s[q], s * 8);
+      buf_load4_lds(live ? rs_s : rs_none, lds + kOffS + buf * kSBytes + (w * nS + q) * 256, vo_s[q], s * 8);
     }
   };
   auto load_stage = [&](int s, int buf) {
@@ -149,28 +154,36 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W
   // activation fragment (m-block j, K-step t): row wm*32*WM + 32j + c32, logical chunk 4h + t.
   // The swizzle depends only on bits 1-4 of the row, those of c32, so one base per K-step serves
   // every m-block (+ j * 4 KiB).
+  // Base addresses are kept opaque to the optimizer, which would otherwise fold each buffer's offset
+  // into a separate register per (buffer, K-step) instead of using the immediate field.
   typedef __attribute__((address_space(3))) const u32x4* lds_frag_ptr;
   const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds;
-  uint32_t a_off[4];
+  constexpr int kImm = 65536;  // ds_read immediate offsets are below 64 KiB
+  constexpr int kFarBuf = (kT256NBuf - 1) * kABytes + 32 * (WM - 1) * 128 >= kImm ? kT256NBuf - 1 : kT256NBuf;
+  uint32_t a_base[4], a_far[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
     const int r = wm * 32 * WM + c32;
-    a_off[t] = (uint32_t)(r * 128 + (((4 * h + t) ^ swz_a(r)) * 16));
+    a_base[t] = lds_base + (uint32_t)(r * 128 + (((4 * h + t) ^ swz_a(r)) * 16));
+    a_far[t] = a_base[t] + kFarBuf * kABytes;
+    asm volatile("" : "+v"(a_base[t]), "+v"(a_far[t]));
   }
   // weight fragment (n-block i): column wn*32*WN + 32i + c32, group h of the stage
-  uint32_t b_off[WN], s_off[WN];
+  uint32_t b_base[WN], s_base[WN];
 #pragma unroll
   for (int i = 0; i < WN; ++i) {
     const int n = wn * 32 * WN + 32 * i + c32;
-    b_off[i] = (uint32_t)(kABytes + n * 32 + 16 * (h ^ swz_b(n)));
-    s_off[i] = (uint32_t)(kABytes + kBBytes + n * 8 + 4 * h);
+    b_base[i] = lds_base + (uint32_t)(kOffB + n * 32 + 16 * (h ^ swz_b(n)));
+    s_base[i] = lds_base + (uint32_t)(kOffS + n * 8 + 4 * h);
+    asm volatile("" : "+v"(b_base[i]), "+v"(s_base[i]));
   }
   auto read_a = [&](int buf, int t, int j) {
-    return *(lds_frag_ptr)(lds_base + buf * kStageBytes + a_off[t] + j * 4096);
+    return buf >= kFarBuf ? *(lds_frag_ptr)(a_far[t] + (buf - kFarBuf) * kABytes + j * 4096)
+                          : *(lds_frag_ptr)(a_base[t] + buf * kABytes + j * 4096);
   };
-  auto read_b = [&](int buf, int i) { return *(lds_frag_ptr)(lds_base + buf * kStageBytes + b_off[i]); };
+  auto read_b = [&](int buf, int i) { return *(lds_frag_ptr)(b_base[i] + buf * kBBytes); };
   auto read_s = [&](int buf, int i) {
-    return *(__attribute__((address_space(3))) const float*)(lds_base + buf * kStageBytes + s_off[i]);
+    return *(__attribute__((address_space(3))) const float*)(s_base[i] + buf * kSBytes);
   };
 
   // Accumulators start as the result of an MFMA on zeros rather than as a zero constant, which
