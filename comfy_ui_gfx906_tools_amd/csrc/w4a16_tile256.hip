@@ -315,90 +315,109 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W
     const int m = m0 + wm * 32 * WM + 32 * j + c32;
     rsj[j] = (rs_p && m < M) ? rs_p[m] : 1.0f;
   }
-  const int act = p.act, odt = p.out_dtype;
-  auto value = [&](int i, int j, int bq, int e) {
-    float v = acc[i][j][4 * bq + e] * rsj[j] + bv[i][bq][e];
-    if (act == kActGeluTanh) v = gelu_tanh(round_to(odt, v));
-    return v;
-  };
-
-  if (odt == kF32) {
-    // fp32: lane (m, h) stores 4 adjacent outputs (16 B) per accumulator quarter
-    const bool vec = (N % 4) == 0 && (((uintptr_t)p.y) & 15) == 0;
+  // The epilogue is instantiated per (activation, output dtype), so that its per-value code has no
+  // branches; one uniform dispatch selects the instance.
+  auto epilogue = [&](auto actc, auto odtc) {
+    constexpr int kAct = decltype(actc)::value, kOdt = decltype(odtc)::value;
+    auto value = [&](int i, int j, int bq, int e) {
+      float v = acc[i][j][4 * bq + e] * rsj[j] + bv[i][bq][e];
+      if constexpr (kAct == kActGeluTanh) v = gelu_tanh(round_to(kOdt, v));
+      return v;
+    };
+    if constexpr (kOdt == kF32) {
+      // fp32: lane (m, h) stores 4 adjacent outputs (16 B) per accumulator quarter
+      const bool vec = (N % 4) == 0 && (((uintptr_t)p.y) & 15) == 0;
 #pragma unroll
-    for (int j = 0; j < WM; ++j) {
-      const int m = m0 + wm * 32 * WM + 32 * j + c32;
-      if (m >= M) continue;
+      for (int j = 0; j < WM; ++j) {
+        const int m = m0 + wm * 32 * WM + 32 * j + c32;
+        if (m >= M) continue;
 #pragma unroll
-      for (int i = 0; i < WN; ++i)
+        for (int i = 0; i < WN; ++i)
 #pragma unroll
-        for (int bq = 0; bq < 4; ++bq) {
-          const int n = n0 + wn * 32 * WN + 32 * i + 8 * bq + 4 * h;
-          float v[4];
+          for (int bq = 0; bq < 4; ++bq) {
+            const int n = n0 + wn * 32 * WN + 32 * i + 8 * bq + 4 * h;
+            float v[4];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) v[e] = value(i, j, bq, e);
-          const size_t off = (size_t)m * N + n;
-          if (vec && n + 3 < N) {
-            *(f32x4*)((float*)p.y + off) = f32x4{v[0], v[1], v[2], v[3]};
-          } else {
+            for (int e = 0; e < 4; ++e) v[e] = value(i, j, bq, e);
+            const size_t off = (size_t)m * N + n;
+            if (vec && n + 3 < N) {
+              *(f32x4*)((float*)p.y + off) = f32x4{v[0], v[1], v[2], v[3]};
+            } else {
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (n + e < N) ((float*)p.y)[off + e] = v[e];
+              for (int e = 0; e < 4; ++e)
+                if (n + e < N) ((float*)p.y)[off + e] = v[e];
+            }
+          }
+      }
+    } else {
+      // 16-bit outputs go through LDS, half a tile (BM/2 rows x BN columns) at a time, so that
+      // each wave stores whole 512-byte row segments with 16-byte lanes instead of 8-byte pieces
+      // of 32 different rows. LDS row r holds 16-byte chunk c at slot c ^ (r & 31): the 8-byte
+      // writes of a wave (32 rows x 2 halves of one chunk) and the 16-byte reads (2 rows x 32
+      // chunks) are both conflict free. The stage buffers are free once every wave is past its
+      // last MFMA and the DMA loads issued for stages past the end (which write zeros) have landed.
+      constexpr int kHalfRows = BM / 2;
+      constexpr int kChunks = BN / 8;  // 16-byte chunks per row
+      static_assert(kHalfRows * BN * 2 <= kT256NBuf * kStageBytes, "half a tile must fit the stage buffers");
+      wait_vmcnt<0>();
+      wait_lgkm();
+      barrier_no_fence();
+      const bool vec = (N % 8) == 0 && (((uintptr_t)p.y) & 15) == 0;
+      static_for<0, 2>([&](auto hc) {
+        constexpr int half = decltype(hc)::value;
+        static_for<0, WM>([&](auto jc) {
+          constexpr int j = decltype(jc)::value;
+          if ((wm * 32 * WM + 32 * j) / kHalfRows != half) return;
+          const int r = wm * 32 * WM + 32 * j - half * kHalfRows + c32;
+#pragma unroll
+          for (int i = 0; i < WN; ++i)
+#pragma unroll
+            for (int bq = 0; bq < 4; ++bq) {
+              const int c = wn * 32 * WN + 32 * i + 8 * bq + 4 * h;  // tile column of the lane's 4 outputs
+              uint32_t lo, hi;
+              if constexpr (kOdt == kBF16) {
+                lo = pack2_bf16(value(i, j, bq, 0), value(i, j, bq, 1));
+                hi = pack2_bf16(value(i, j, bq, 2), value(i, j, bq, 3));
+              } else {
+                lo = pack2_f16(value(i, j, bq, 0), value(i, j, bq, 1));
+                hi = pack2_f16(value(i, j, bq, 2), value(i, j, bq, 3));
+              }
+              typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+              *(u32x2*)(lds + r * (BN * 2) + (((c >> 3) ^ (r & 31)) << 4) + (c & 7) * 2) = u32x2{lo, hi};
+            }
+        });
+        barrier_no_fence();
+#pragma unroll
+        for (int k = 0; k < kHalfRows * kChunks / (64 * kWaves); ++k) {
+          const int q = threadIdx.x + k * 64 * kWaves;
+          const int r = q / kChunks, c = q % kChunks;
+          const u32x4 v = *(const u32x4*)(lds + r * (BN * 2) + ((c ^ (r & 31)) << 4));
+          const int m = m0 + half * kHalfRows + r, n = n0 + 8 * c;
+          if (m < M && n < N) {
+            uint16_t* dst = (uint16_t*)p.y + (size_t)m * N + n;
+            if (vec && n + 8 <= N) {
+              *(u32x4*)dst = v;
+            } else {
+              for (int e = 0; e < 8 && n + e < N; ++e) dst[e] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
+            }
           }
         }
+        if constexpr (half == 0) barrier_no_fence();
+      });
     }
-    return;
+  };
+  const bool gelu = p.act == kActGeluTanh;
+  switch (p.out_dtype) {
+    case kF32:
+      gelu ? epilogue(ic<kActGeluTanh>{}, ic<kF32>{}) : epilogue(ic<kActNone>{}, ic<kF32>{});
+      break;
+    case kF16:
+      gelu ? epilogue(ic<kActGeluTanh>{}, ic<kF16>{}) : epilogue(ic<kActNone>{}, ic<kF16>{});
+      break;
+    default:
+      gelu ? epilogue(ic<kActGeluTanh>{}, ic<kBF16>{}) : epilogue(ic<kActNone>{}, ic<kBF16>{});
+      break;
   }
-
-  // 16-bit outputs go through LDS, half a tile (BM/2 rows x BN columns, 64 KiB) at a time, so that
-  // each wave stores whole 512-byte row segments with 16-byte lanes instead of 8-byte pieces of
-  // 32 different rows. LDS row r holds 16-byte chunk c at slot c ^ (r & 31): the 8-byte writes of
-  // a wave (32 rows x 2 halves of one chunk) and the 16-byte reads (2 rows x 32 chunks) are both
-  // conflict free. The stage buffers are free once every wave is past its last MFMA and the DMA
-  // loads issued for stages past the end (which write zeros) have landed.
-  constexpr int kHalfRows = BM / 2;
-  constexpr int kChunks = BN / 8;  // 16-byte chunks per row
-  static_assert(kHalfRows * BN * 2 <= kT256NBuf * kStageBytes, "half a tile must fit the stage buffers");
-  wait_vmcnt<0>();
-  wait_lgkm();
-  barrier_no_fence();
-  const bool bf_out = odt == kBF16;
-  const bool vec = (N % 8) == 0 && (((uintptr_t)p.y) & 15) == 0;
-  static_for<0, 2>([&](auto hc) {
-    constexpr int half = decltype(hc)::value;
-#pragma unroll
-    for (int j = 0; j < WM; ++j) {
-      const int rt = wm * 32 * WM + 32 * j;  // first tile row of block j
-      if (rt / kHalfRows != half) continue;
-      const int r = rt - half * kHalfRows + c32;
-#pragma unroll
-      for (int i = 0; i < WN; ++i)
-#pragma unroll
-        for (int bq = 0; bq < 4; ++bq) {
-          const int c = wn * 32 * WN + 32 * i + 8 * bq + 4 * h;  // tile column of the lane's 4 outputs
-          const uint32_t lo = bf_out ? pack2_bf16(value(i, j, bq, 0), value(i, j, bq, 1))
-                                     : pack2_f16(value(i, j, bq, 0), value(i, j, bq, 1));
-          const uint32_t hi = bf_out ? pack2_bf16(value(i, j, bq, 2), value(i, j, bq, 3))
-                                     : pack2_f16(value(i, j, bq, 2), value(i, j, bq, 3));
-          typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-          *(u32x2*)(lds + r * (BN * 2) + (((c >> 3) ^ (r & 31)) << 4) + (c & 7) * 2) = u32x2{lo, hi};
-        }
-    }
-    barrier_no_fence();
-    for (int q = threadIdx.x; q < kHalfRows * kChunks; q += 64 * kWaves) {
-      const int r = q / kChunks, c = q % kChunks;
-      const u32x4 v = *(const u32x4*)(lds + r * (BN * 2) + ((c ^ (r & 31)) << 4));
-      const int m = m0 + half * kHalfRows + r, n = n0 + 8 * c;
-      if (m >= M || n >= N) continue;
-      uint16_t* dst = (uint16_t*)p.y + (size_t)m * N + n;
-      if (vec && n + 8 <= N) {
-        *(u32x4*)dst = v;
-      } else {
-        for (int e = 0; e < 8 && n + e < N; ++e) dst[e] = (uint16_t)(v[e >> 1] >> (16 * (e & 1)));
-      }
-    }
-    if constexpr (half == 0) barrier_no_fence();
-  });
 }
 
 template <bool kBf16, int kWavesM, int kWavesN, int WM, int WN>
