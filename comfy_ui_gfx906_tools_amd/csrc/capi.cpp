@@ -87,9 +87,10 @@ size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 // M <= 128, else a 256 x 256 tile when its tiles fill every CU at least once, else 128-row tiles
 // (whose last wave of tiles the planner may cut into K pieces).
 constexpr int kCfgTile256 = 4;
-constexpr int kCfgLast = kCfgTile256 + kTile256Variants - 1;
+constexpr int kCfgGemv = kCfgTile256 + kTile256Variants;  // 7: rows <= 4, VALU dot products
+constexpr int kCfgLast = kCfgGemv;
 constexpr int kCfgTile256Auto = kCfgTile256 + 1;
-bool is_tile256(int cfg) { return cfg >= kCfgTile256 && cfg <= kCfgLast; }
+bool is_tile256(int cfg) { return cfg >= kCfgTile256 && cfg < kCfgTile256 + kTile256Variants; }
 
 // Tiles of the 256 x 256 kernel that run whole: every full round of CUs; the remaining tiles are
 // cut into 128-row halves when their halves fit in one more round, else they run whole too.
@@ -111,8 +112,16 @@ bool prefer_tile256(int64_t M, int64_t N, int64_t K, int cus) {
   return t256 <= t128;
 }
 
-// (An explicit K split, splits >= 2, needs the 4-wave kernel: the 256 x 256 kernel has none.)
-int w4a16_cfg_for(int64_t M, int64_t N, int64_t K, int splits, int cus) {
+// Up to 4 rows of 16-bit activations go to the VALU kernel (configuration 7), read as they are.
+// (An explicit K split, splits >= 2, needs the 4-wave kernel: the 256 x 256 kernel and the VALU
+// kernel have none.)
+bool gemv_fits(int x_dtype, int64_t M, int64_t K) {
+  const int64_t mp = M <= 1 ? 1 : M <= 2 ? 2 : 4;  // rows the kernel instance handles
+  return M <= kGemvMaxM && K <= kGemvMaxK && mp * K <= kGemvMaxMK && (x_dtype == QL_BF16 || x_dtype == QL_F16);
+}
+
+int w4a16_cfg_for(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, int cus) {
+  if (splits < 2 && gemv_fits(x_dtype, M, K)) return kCfgGemv;
   if (M <= 16) return 3;
   if (M <= 64) return 2;
   if (M <= 128) return 1;
@@ -121,10 +130,14 @@ int w4a16_cfg_for(int64_t M, int64_t N, int64_t K, int splits, int cus) {
 
 W4A16Plan plan_w4a16(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, int flags, int cus) {
   W4A16Plan pl{};
-  pl.prepass = x_dtype == QL_F32 || (x_dtype == QL_BF16 && !(flags & QL_W4A16_BF16_MFMA));
   const int forced = (flags & QL_W4A16_CFG_MASK) >> QL_W4A16_CFG_SHIFT;
-  pl.cfg = forced ? forced - 1 : w4a16_cfg_for(M, N, K, splits, cus);
-  if (is_tile256(pl.cfg)) {
+  pl.cfg = forced ? forced - 1 : w4a16_cfg_for(x_dtype, M, N, K, splits, cus);
+  pl.prepass = pl.cfg != kCfgGemv && (x_dtype == QL_F32 || (x_dtype == QL_BF16 && !(flags & QL_W4A16_BF16_MFMA)));
+  if (pl.cfg == kCfgGemv) {
+    pl.BM = 4;
+    pl.BN = 16;
+    pl.stages = 1;
+  } else if (is_tile256(pl.cfg)) {
     pl.BM = pl.BN = 256;
     pl.stages = (int)(K / 64);
   } else {
@@ -138,7 +151,9 @@ W4A16Plan plan_w4a16(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, i
   const int tiles = pl.tiles_m * pl.tiles_n;
   pl.dp_tiles = tiles;
   pl.ksplit = 1;
-  if (is_tile256(pl.cfg)) {
+  if (pl.cfg == kCfgGemv) {
+    // one launch, no K split
+  } else if (is_tile256(pl.cfg)) {
     pl.dp_tiles = splits == 1 ? tiles : (int)tile256_whole(tiles, cus);
   } else if (splits >= 2 && tiles <= kMaxCutTiles) {
     pl.ksplit = std::min(splits, pl.stages);
@@ -165,7 +180,7 @@ W4A16Plan plan_w4a16(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, i
     }
   }
   pl.grid = pl.dp_tiles + (tiles - pl.dp_tiles) * pl.ksplit;
-  const size_t partial_bytes = (pl.dp_tiles < tiles && !is_tile256(pl.cfg))
+  const size_t partial_bytes = (pl.dp_tiles < tiles && !is_tile256(pl.cfg) && pl.cfg != kCfgGemv)
                                    ? (size_t)(tiles - pl.dp_tiles) * pl.ksplit * pl.BM * pl.BN * sizeof(float)
                                    : 0;
   pl.off_row_scale = 0;
@@ -233,6 +248,13 @@ int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const float* r
     if (forced && is_tile256(forced - 1) && splits >= 2)
       return fail(QL_ERR_ARG, "kernel configuration %d runs whole tiles only (splits 0 or 1), got splits=%d",
                   forced - 1, splits);
+    if (forced == kCfgGemv + 1 && !gemv_fits(x_dtype, M, K))
+      return fail(QL_ERR_SHAPE, "kernel configuration %d needs M <= %d, K <= %d (K <= %d for M > 2) and "
+                  "bfloat16/float16 x; got M=%lld K=%lld x %s", kCfgGemv, kGemvMaxM, kGemvMaxK, kGemvMaxMK / 4,
+                  (long long)M, (long long)K, dtype_name(x_dtype));
+    if (forced == kCfgGemv + 1 && splits >= 2)
+      return fail(QL_ERR_ARG, "kernel configuration %d has no K split (splits 0 or 1), got splits=%d", kCfgGemv,
+                  splits);
   }
   if (row_scale && x_dtype != QL_F16)
     return fail(QL_ERR_ARG, "row_scale is only accepted with float16 x (from qlinear_rows_to_f16), got %s",
@@ -271,13 +293,15 @@ int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const float* r
   p.K = (int)K;
   p.out_dtype = out_dtype;
   p.act = (flags & QL_W4A16_GELU_TANH) ? kActGeluTanh : kActNone;
+  p.cus = cus;
   p.tiles_m = pl.tiles_m;
   p.tiles_n = pl.tiles_n;
   p.stages = pl.stages;
   p.dp_tiles = pl.dp_tiles;
   p.ksplit = pl.ksplit;
   const bool bf16_mfma = x_dtype == QL_BF16 && !pl.prepass;
-  const hipError_t e = is_tile256(pl.cfg)
+  const hipError_t e = pl.cfg == kCfgGemv ? w4a16_gemv_launch(x_dtype == QL_BF16, p, (hipStream_t)stream)
+                       : is_tile256(pl.cfg)
                            ? w4a16_tile256_launch(pl.cfg - kCfgTile256, bf16_mfma, p, (hipStream_t)stream)
                            : w4a16_launch(pl.cfg, bf16_mfma, p, (hipStream_t)stream);
   if (e != hipSuccess) return fail(QL_ERR_LAUNCH, "w4a16 launch failed: %s", hipGetErrorString(e));

@@ -25,6 +25,7 @@ struct W4A16Params {
   int dp_tiles;          // tiles processed whole, one workgroup each
   int ksplit;            // K pieces of every tile past dp_tiles (>= 2 when any)
   int tile_base;         // 256 x 256 kernel: first tile of the launch (set by the launcher)
+  int cus;               // compute units of the device (grid sizing)
 };
 
 struct W4A16Config {
@@ -44,6 +45,10 @@ hipError_t w4a16_launch(int cfg, bool bf16, const W4A16Params& p, hipStream_t st
 // p.dp_tiles tiles (grouped order) run whole, the rest as two 128-row halves each (second launch).
 constexpr int kTile256Variants = 3;
 hipError_t w4a16_tile256_launch(int variant, bool bf16, const W4A16Params& p, hipStream_t stream);
+// Activation rows up to 4, bf16 / fp16 x as is, K <= 8192 and M * K <= 16384 (w4a16_gemv.hip):
+// VALU dot products on exact integer codes, columns streamed by about two waves per SIMD.
+constexpr int kGemvMaxM = 4, kGemvMaxK = 8192, kGemvMaxMK = 16384;
+hipError_t w4a16_gemv_launch(bool bf16, const W4A16Params& p, hipStream_t stream);
 hipError_t rows_to_scaled_f16_launch(int dtype, const void* x, void* x16, float* row_scale, int64_t M,
                                      int64_t K, hipStream_t stream);
 

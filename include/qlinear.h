@@ -78,8 +78,10 @@ int qlinear_abi_version(void);
 #define QL_W4A16_GELU_TANH 2
 /* flags bits 8-11: 0 = automatic kernel choice, c + 1 = force kernel configuration c
  * (0-3: 256 / 128 / 64 / 16-row x 256-column tiles, 4 waves; 4-6: 256 x 256 tiles with 8 waves
- * as 2 x 4, 8 waves as 1 x 8, 4 waves as 1 x 4, K % 64 == 0, whole tiles only). For tuning and
- * tests; results agree to rounding. */
+ * as 2 x 4, 8 waves as 1 x 8, 4 waves as 1 x 4, K % 64 == 0, whole tiles only; 7: M <= 4,
+ * K <= 8192, bfloat16/float16 x read as given, VALU dot products on the exact integer codes with
+ * the group scale applied in fp32 -- the automatic choice for such M). For tuning and tests;
+ * results agree to rounding. */
 #define QL_W4A16_CFG_SHIFT 8
 #define QL_W4A16_CFG_MASK (0xF << QL_W4A16_CFG_SHIFT)
 #define QL_W4A16_CFG(c) (((c) + 1) << QL_W4A16_CFG_SHIFT)

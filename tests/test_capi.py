@@ -92,9 +92,13 @@ def test_w4a16_argument_checks(lib):
     # forced kernel configurations (flags bits 8-11 = configuration + 1): 0-6 exist; the 256 x 256
     # configurations 4-6 need K % 64 == 0 and whole tiles
     cfg = lambda c: (c + 1) << 8  # noqa: E731
-    assert f(2, 2, None, None, None, None, None, None, 0, 64, 64, 0, cfg(7), None, 0, None) == QL_ERR_ARG
-    assert "configuration 7 does not exist" in _err(lib)
-    for c in range(7):
+    assert f(2, 2, None, None, None, None, None, None, 0, 64, 64, 0, cfg(8), None, 0, None) == QL_ERR_ARG
+    assert "configuration 8 does not exist" in _err(lib)
+    # configuration 7 (VALU, M <= 4): 16-bit x, K <= 8192
+    assert f(0, 2, None, None, None, None, None, None, 0, 64, 64, 0, cfg(7), None, 0, None) == QL_ERR_SHAPE
+    assert f(2, 2, None, None, None, None, None, None, 5, 64, 64, 0, cfg(7), None, 0, None) == QL_ERR_SHAPE
+    assert f(2, 2, None, None, None, None, None, None, 1, 64, 8224, 0, cfg(7), None, 0, None) == QL_ERR_SHAPE
+    for c in range(8):
         assert f(2, 2, None, None, None, None, None, None, 0, 64, 64, 0, cfg(c), None, 0, None) == QL_OK
     for c in (4, 5, 6):
         assert f(2, 2, None, None, None, None, None, None, 0, 64, 96, 0, cfg(c), None, 0, None) == QL_ERR_SHAPE

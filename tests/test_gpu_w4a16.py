@@ -263,3 +263,73 @@ def test_w4a16_fused_gelu_matches_unfused(cfg, out_dtype):
     else:
         assert (np.abs(f - exact) <= 1e-5 * np.abs(exact) + 1e-6).all(), f"max diff {np.abs(f - exact).max():.3e}"
         assert (np.abs(f - r_torch) <= 1e-5 * np.abs(r_torch) + 1e-6).all()
+
+
+GEMV_CFG = 7
+
+
+@pytest.mark.parametrize("M", [1, 2, 3, 4])
+@pytest.mark.parametrize("N,K", [(1, 32), (3, 96), (17, 2048), (100, 4096), (257, 3072), (64, 8192)])
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
+def test_w4a16_gemv_vs_oracle(M, N, K, xdt):
+    """Configuration 7 (M <= 4, VALU dot products on exact codes): ragged N (wave columns past N),
+    K with partial last groups-per-lane rounds (K = 3072: 96 groups over 64 lanes), bias, fp32 out;
+    within the gate against the fp64 oracle, deterministic. The codes and x enter exactly and the
+    scale is applied in fp32, so the error is far below the gate (checked at 2e-4)."""
+    print(f"case gemv M={M} N={N} K={K} x={xdt}", flush=True)
+    x, wq, ws = seeded_linear(M, N, K, seed=7 * M + N + K, x_dtype=xdt)
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(M))
+    if M > 2 and K > 4096:  # the kernel keeps M x K activations in registers: M * K <= 16384
+        with pytest.raises(RuntimeError, match="K <= 4096 for M > 2"):
+            _run_cfg(x, wq, ws, bias, cfg=GEMV_CFG)
+        return
+    y1 = _run_cfg(x, wq, ws, bias, cfg=GEMV_CFG)
+    y2 = _run_cfg(x, wq, ws, bias, cfg=GEMV_CFG)
+    assert torch.equal(y1, y2), "not deterministic"
+    ref = orc.w4a16_reference(to_np_f32(x), wq.numpy(), ws.numpy(), bias.numpy())
+    err = rel_max_err(to_np_f32(y1), ref)
+    assert err <= 2e-4, f"max rel err {err:.3e}"
+
+
+def test_w4a16_gemv_exact_on_integer_grid():
+    """Integer x, codes in [-8, 7], power-of-two scales: every partial sum is exact in fp32, so the
+    VALU kernel must equal the fp64 oracle exactly (both dtypes)."""
+    M, N, K = 4, 70, 2048
+    g = np.random.default_rng(41)
+    codes = g.integers(-8, 8, (N, K))
+    nib = (codes & 0xF).astype(np.uint8)
+    packed = (nib[:, 0::2] | (nib[:, 1::2] << 4)).view(np.int8)
+    scale = (2.0 ** g.integers(-6, 0, (N, K // 32))).astype(np.float32)
+    for xdt in (torch.bfloat16, torch.float16):
+        x = torch.from_numpy(g.integers(-4, 5, (M, K)).astype(np.float32)).to(xdt)
+        y = to_np_f32(_run_cfg(x, torch.from_numpy(packed), torch.from_numpy(scale), cfg=GEMV_CFG))
+        ref = orc.w4a16_reference(to_np_f32(x), packed, scale)
+        assert np.array_equal(y.astype(np.float64), ref), f"{xdt}: max abs diff {np.abs(y - ref).max()}"
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16])
+def test_w4a16_gemv_16bit_out_gelu_and_row_scale(out_dtype):
+    """16-bit outputs (1 ulp + gate), the fused GELU (1 ulp of the exact GELU of the plain output),
+    and fp16 x staged by rows_to_f16 with its row scale, through configuration 7 and the automatic
+    choice (which takes configuration 7 for M <= 4)."""
+    from comfy_ui_gfx906_tools_amd import _lib as L
+    M, N, K = 3, 300, 3072
+    x, wq, ws = seeded_linear(M, N, K, seed=51)
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(6)).to(out_dtype)
+    ref = orc.w4a16_reference(to_np_f32(x), wq.numpy(), ws.numpy(), to_np_f32(bias)).astype(np.float32)
+    name = "bfloat16" if out_dtype == torch.bfloat16 else "float16"
+    ref_r = orc.round_to_dtype(ref, name)
+    ulp = bf16_ulp(ref_r) if out_dtype == torch.bfloat16 else f16_ulp(ref_r)
+    for cfg in (GEMV_CFG, None):
+        y = to_np_f32(_run_cfg(x, wq, ws, bias, out_dtype=out_dtype, cfg=cfg))
+        assert (np.abs(y - ref_r) <= ulp + 2e-4 * np.abs(ref).max()).all()
+    plain = _run_cfg(x, wq, ws, bias, out_dtype=out_dtype, cfg=GEMV_CFG)
+    fused = L.w4a16_gemm(x.to(DEV), wq.to(DEV), ws.to(DEV), bias.to(DEV), out_dtype=out_dtype, config=GEMV_CFG,
+                         gelu=True)
+    e = orc.round_to_dtype(_gelu_tanh_f64(to_np_f32(plain)).astype(np.float32), name)
+    ue = bf16_ulp(e) if out_dtype == torch.bfloat16 else f16_ulp(e)
+    assert (np.abs(to_np_f32(fused) - e) <= ue).all()
+    x16, rs = L.rows_to_f16(x.to(DEV))
+    y = to_np_f32(L.w4a16_gemm(x16, wq.to(DEV), ws.to(DEV), bias.to(DEV), out_dtype=out_dtype, row_scale=rs,
+                               config=GEMV_CFG))
+    assert (np.abs(y - ref_r) <= ulp + 2e-4 * np.abs(ref).max()).all()
