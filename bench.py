@@ -166,7 +166,7 @@ def main():
     achieved = flops_launch / (avg_ms["fc1"] * 1e-3) / 1e12
 
     traffic = None
-    tpath = os.path.join(HERE, "profiles", "w4a16_gemm_c2_fc1_traffic.json")
+    tpath = os.path.join(HERE, "profiles", "w4a16_tile256_c2_fc1_traffic.json")
     if os.path.exists(tpath):
         with open(tpath) as f:
             traffic = json.load(f).get("hbm_bytes_per_launch")
