@@ -366,8 +366,12 @@ int qlinear_w8a8_gemm(int out_dtype, const int8_t* xq, const float* x_scale, con
   if (!xq || !wq || !y) return fail(QL_ERR_ARG, "null xq / wq / y pointer");
   if (out_dtype != QL_I32 && (!x_scale || !w_scale)) return fail(QL_ERR_ARG, "null x_scale / w_scale pointer");
   if (!aligned16(xq) || !aligned16(wq)) return fail(QL_ERR_ALIGN, "xq and wq must be 16-byte aligned");
-  const int cfg = M <= 16 ? 3 : M <= 64 ? 2 : M <= 128 ? 1 : 0;
+  // M > 128: the 256 x 256-tile kernel (32-bit buffer offsets: 256 * K bytes per operand tile);
+  // skinny M: the 16 / 64 / 128-row tiles
+  const bool big = M > 128 && K * kW8A8Tile256 <= INT32_MAX;
+  const int cfg = M <= 16 ? 3 : M <= 64 ? 2 : 1;
   const W8A8Config& c = w8a8_config(cfg);
+  const int BM = big ? kW8A8Tile256 : c.BM, BN = big ? kW8A8Tile256 : c.BN;
   W8A8Params p{};
   p.xq = xq;
   p.sx = x_scale;
@@ -379,10 +383,11 @@ int qlinear_w8a8_gemm(int out_dtype, const int8_t* xq, const float* x_scale, con
   p.N = (int)N;
   p.K = (int)K;
   p.out_dtype = out_dtype;
-  p.tiles_m = (int)((M + c.BM - 1) / c.BM);
-  p.tiles_n = (int)((N + c.BN - 1) / c.BN);
+  p.tiles_m = (int)((M + BM - 1) / BM);
+  p.tiles_n = (int)((N + BN - 1) / BN);
   p.stages = (int)((K + 255) / 256);
-  const hipError_t e = w8a8_launch(cfg, p, p.tiles_m * p.tiles_n, (hipStream_t)stream);
+  const hipError_t e = big ? w8a8_tile256_launch(p, (hipStream_t)stream)
+                           : w8a8_launch(cfg, p, p.tiles_m * p.tiles_n, (hipStream_t)stream);
   if (e != hipSuccess) return fail(QL_ERR_LAUNCH, "w8a8 launch failed: %s", hipGetErrorString(e));
   return ok();
 }

@@ -70,6 +70,9 @@ struct W8A8Config {
 };
 const W8A8Config& w8a8_config(int id);
 hipError_t w8a8_launch(int cfg, const W8A8Params& p, int grid, hipStream_t stream);
+// 256 x 256-tile int8 MFMA kernel for M > 128 (grid = tiles_m * tiles_n of 256 x 256)
+constexpr int kW8A8Tile256 = 256;
+hipError_t w8a8_tile256_launch(const W8A8Params& p, hipStream_t stream);
 
 hipError_t quantize_int4_launch(int dtype, int rule, const void* x, void* packed, float* scale,
                                 int64_t rows, int64_t K, hipStream_t stream);

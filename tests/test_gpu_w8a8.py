@@ -31,7 +31,10 @@ def test_quantize_int8_per_token_matches_oracle(M, K, dt):
     assert np.array_equal(q.cpu().numpy(), q_ref)
 
 
-SHAPES = [(1, 256, 64), (5, 300, 192), (64, 512, 3072), (200, 1000, 4096), (257, 256, 256)]
+# M <= 128 runs the 16 / 64 / 128-row kernel, M > 128 the 256 x 256-tile kernel (ragged M and N,
+# K of 1, 3, 4 and 5 stages of 64, 64-row and 16-row remainders of a tile)
+SHAPES = [(1, 256, 64), (5, 300, 192), (64, 512, 3072), (200, 1000, 4096), (257, 256, 256), (129, 17, 64),
+          (300, 520, 192), (513, 257, 320), (256, 768, 4224)]
 
 
 @pytest.mark.parametrize("M,N,K", SHAPES)
@@ -46,9 +49,11 @@ def test_w8a8_accumulators_bit_exact(M, N, K):
     assert np.array_equal(acc.cpu().numpy().astype(np.int64), ref)
 
 
-def test_w8a8_extreme_values_bit_exact():
+@pytest.mark.parametrize("M", [32, 300])
+def test_w8a8_extreme_values_bit_exact(M):
     """All +-127 / -128 operands: the largest-magnitude accumulators the format allows."""
-    M, N, K = 32, 64, 12288
+    N, K = 64, 12288
+    print(f"case w8a8 extreme M={M}", flush=True)
     a = np.full((M, K), -128, np.int8)
     a[1::2] = 127
     b = np.full((N, K), -128, np.int8)
@@ -60,9 +65,10 @@ def test_w8a8_extreme_values_bit_exact():
 
 @pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16, torch.float16])
 @pytest.mark.parametrize("with_bias", [False, True])
-def test_w8a8_epilogue_bit_exact(out_dtype, with_bias):
-    M, N, K = 130, 320, 1024
-    print(f"case w8a8 epilogue {out_dtype} bias={with_bias}", flush=True)
+@pytest.mark.parametrize("M,N", [(100, 320), (130, 320), (300, 261)])
+def test_w8a8_epilogue_bit_exact(out_dtype, with_bias, M, N):
+    K = 1024
+    print(f"case w8a8 epilogue M={M} N={N} {out_dtype} bias={with_bias}", flush=True)
     g = torch.Generator().manual_seed(4)
     x = torch.randn(M, K, generator=g).to(torch.bfloat16)
     w = torch.randn(N, K, generator=g) * 0.02
