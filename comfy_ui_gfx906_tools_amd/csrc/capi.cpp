@@ -83,12 +83,15 @@ size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
 
 // Kernel configurations: 0-3 are w4a16_gemm_kernel tiles of 256 / 128 / 64 / 16 rows x 256
 // columns (4 waves side by side); 4-6 are the w4a16_tile256_kernel variants 0-2 (256 x 256
-// tiles, whole tiles, K % 64 == 0). Automatic choice: the smallest tile that covers M for
-// M <= 128, else a 256 x 256 tile when its tiles fill every CU at least once, else 128-row tiles
-// (whose last wave of tiles the planner may cut into K pieces).
+// tiles, whole tiles, K % 64 == 0); 7 is the VALU kernel for M <= 4 and 8 the MFMA kernel for
+// M <= 16 (both read 16-bit x as is). Automatic choice: 7 for one row, 8 for up to 16 rows where
+// it applies, then the smallest tile that covers M for M <= 128, else a 256 x 256 tile when its
+// tiles fill every CU at least once, else 128-row tiles (whose last wave of tiles the planner may
+// cut into K pieces).
 constexpr int kCfgTile256 = 4;
 constexpr int kCfgGemv = kCfgTile256 + kTile256Variants;  // 7: rows <= 4, VALU dot products
-constexpr int kCfgLast = kCfgGemv;
+constexpr int kCfgSkinny = kCfgGemv + 1;                  // 8: rows <= 16, MFMA, K split in-workgroup
+constexpr int kCfgLast = kCfgSkinny;
 constexpr int kCfgTile256Auto = kCfgTile256 + 1;
 bool is_tile256(int cfg) { return cfg >= kCfgTile256 && cfg < kCfgTile256 + kTile256Variants; }
 
@@ -120,8 +123,22 @@ bool gemv_fits(int x_dtype, int64_t M, int64_t K) {
   return M <= kGemvMaxM && K <= kGemvMaxK && mp * K <= kGemvMaxMK && (x_dtype == QL_BF16 || x_dtype == QL_F16);
 }
 
-int w4a16_cfg_for(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, int cus) {
-  if (splits < 2 && gemv_fits(x_dtype, M, K)) return kCfgGemv;
+// Up to 16 rows of 16-bit activations, K % 128 == 0 and K <= 4096: the MFMA kernel for skinny M
+// (configuration 8), also read as they are.
+bool skinny_fits(int x_dtype, int64_t M, int64_t N, int64_t K) {
+  return M <= kSkinnyMaxM && K % 128 == 0 && K <= kSkinnyMaxK && (N + 64) * (K / 2) < INT32_MAX &&
+         (x_dtype == QL_BF16 || x_dtype == QL_F16);
+}
+
+// One row: the VALU kernel (8.8 us vs 10.6 us at K=4096 N=10240); 2-16 rows: the MFMA kernel
+// (4 rows: 10.9 us vs 14.9 us; 16 rows: 14.5 us vs 22.6 us for the 16-row tile kernel).
+// QL_W4A16_BF16_MFMA asks for the reference's bf16-rounded weights, which only the tile kernels
+// compute; 7 and 8 use the exact codes and are skipped then.
+int w4a16_cfg_for(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, int flags, int cus) {
+  const bool exact_ok = splits < 2 && !(flags & QL_W4A16_BF16_MFMA);
+  if (exact_ok && M <= 1 && gemv_fits(x_dtype, M, K)) return kCfgGemv;
+  if (exact_ok && skinny_fits(x_dtype, M, N, K)) return kCfgSkinny;
+  if (exact_ok && gemv_fits(x_dtype, M, K)) return kCfgGemv;
   if (M <= 16) return 3;
   if (M <= 64) return 2;
   if (M <= 128) return 1;
@@ -131,11 +148,16 @@ int w4a16_cfg_for(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, int 
 W4A16Plan plan_w4a16(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, int flags, int cus) {
   W4A16Plan pl{};
   const int forced = (flags & QL_W4A16_CFG_MASK) >> QL_W4A16_CFG_SHIFT;
-  pl.cfg = forced ? forced - 1 : w4a16_cfg_for(x_dtype, M, N, K, splits, cus);
-  pl.prepass = pl.cfg != kCfgGemv && (x_dtype == QL_F32 || (x_dtype == QL_BF16 && !(flags & QL_W4A16_BF16_MFMA)));
+  pl.cfg = forced ? forced - 1 : w4a16_cfg_for(x_dtype, M, N, K, splits, flags, cus);
+  const bool direct = pl.cfg == kCfgGemv || pl.cfg == kCfgSkinny;  // 16-bit x read as is
+  pl.prepass = !direct && (x_dtype == QL_F32 || (x_dtype == QL_BF16 && !(flags & QL_W4A16_BF16_MFMA)));
   if (pl.cfg == kCfgGemv) {
     pl.BM = 4;
     pl.BN = 16;
+    pl.stages = 1;
+  } else if (pl.cfg == kCfgSkinny) {
+    pl.BM = 16;
+    pl.BN = 32;
     pl.stages = 1;
   } else if (is_tile256(pl.cfg)) {
     pl.BM = pl.BN = 256;
@@ -151,8 +173,8 @@ W4A16Plan plan_w4a16(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, i
   const int tiles = pl.tiles_m * pl.tiles_n;
   pl.dp_tiles = tiles;
   pl.ksplit = 1;
-  if (pl.cfg == kCfgGemv) {
-    // one launch, no K split
+  if (direct) {
+    // one launch, no K split across workgroups
   } else if (is_tile256(pl.cfg)) {
     pl.dp_tiles = splits == 1 ? tiles : (int)tile256_whole(tiles, cus);
   } else if (splits >= 2 && tiles <= kMaxCutTiles) {
@@ -180,7 +202,7 @@ W4A16Plan plan_w4a16(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, i
     }
   }
   pl.grid = pl.dp_tiles + (tiles - pl.dp_tiles) * pl.ksplit;
-  const size_t partial_bytes = (pl.dp_tiles < tiles && !is_tile256(pl.cfg) && pl.cfg != kCfgGemv)
+  const size_t partial_bytes = (pl.dp_tiles < tiles && !is_tile256(pl.cfg) && !direct)
                                    ? (size_t)(tiles - pl.dp_tiles) * pl.ksplit * pl.BM * pl.BN * sizeof(float)
                                    : 0;
   pl.off_row_scale = 0;
@@ -252,8 +274,12 @@ int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const float* r
       return fail(QL_ERR_SHAPE, "kernel configuration %d needs M <= %d, K <= %d (K <= %d for M > 2) and "
                   "bfloat16/float16 x; got M=%lld K=%lld x %s", kCfgGemv, kGemvMaxM, kGemvMaxK, kGemvMaxMK / 4,
                   (long long)M, (long long)K, dtype_name(x_dtype));
-    if (forced == kCfgGemv + 1 && splits >= 2)
-      return fail(QL_ERR_ARG, "kernel configuration %d has no K split (splits 0 or 1), got splits=%d", kCfgGemv,
+    if (forced == kCfgSkinny + 1 && !skinny_fits(x_dtype, M, N, K))
+      return fail(QL_ERR_SHAPE, "kernel configuration %d needs M <= %d, K %% 128 == 0, K <= %d and "
+                  "bfloat16/float16 x; got M=%lld N=%lld K=%lld x %s", kCfgSkinny, kSkinnyMaxM, kSkinnyMaxK,
+                  (long long)M, (long long)N, (long long)K, dtype_name(x_dtype));
+    if ((forced == kCfgGemv + 1 || forced == kCfgSkinny + 1) && splits >= 2)
+      return fail(QL_ERR_ARG, "kernel configuration %d has no K split (splits 0 or 1), got splits=%d", forced - 1,
                   splits);
   }
   if (row_scale && x_dtype != QL_F16)
@@ -300,7 +326,8 @@ int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const float* r
   p.dp_tiles = pl.dp_tiles;
   p.ksplit = pl.ksplit;
   const bool bf16_mfma = x_dtype == QL_BF16 && !pl.prepass;
-  const hipError_t e = pl.cfg == kCfgGemv ? w4a16_gemv_launch(x_dtype == QL_BF16, p, (hipStream_t)stream)
+  const hipError_t e = pl.cfg == kCfgGemv     ? w4a16_gemv_launch(x_dtype == QL_BF16, p, (hipStream_t)stream)
+                       : pl.cfg == kCfgSkinny ? w4a16_skinny_launch(x_dtype == QL_BF16, p, (hipStream_t)stream)
                        : is_tile256(pl.cfg)
                            ? w4a16_tile256_launch(pl.cfg - kCfgTile256, bf16_mfma, p, (hipStream_t)stream)
                            : w4a16_launch(pl.cfg, bf16_mfma, p, (hipStream_t)stream);

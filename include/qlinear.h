@@ -61,7 +61,8 @@ int qlinear_abi_version(void);
  *             weights dequantize to fp16 -- 8x less weight rounding than bf16 -- and the
  *             epilogue scales back exactly. With QL_W4A16_BF16_MFMA in flags, bf16 x is fed to
  *             bf16 MFMA directly (the reference's own bf16 dequant-then-matmul numerics; no
- *             staging pass). row_scale must be NULL for these dtypes.
+ *             staging pass; the automatic choice then stays on the tile kernels 0-6).
+ *             row_scale must be NULL for these dtypes.
  *   out_dtype QL_F32, QL_F16 or QL_BF16; bias (optional, may be NULL) has dtype out_dtype
  *   K % 32 == 0, K >= 32; M >= 0 (M == 0 launches nothing)
  *   splits    0 = automatic (under-filled last waves are cut into K pieces),
@@ -80,8 +81,10 @@ int qlinear_abi_version(void);
  * (0-3: 256 / 128 / 64 / 16-row x 256-column tiles, 4 waves; 4-6: 256 x 256 tiles with 8 waves
  * as 2 x 4, 8 waves as 1 x 8, 4 waves as 1 x 4, K % 64 == 0, whole tiles only; 7: M <= 4,
  * K <= 8192, bfloat16/float16 x read as given, VALU dot products on the exact integer codes with
- * the group scale applied in fp32 -- the automatic choice for such M). For tuning and tests;
- * results agree to rounding. */
+ * the group scale applied in fp32 -- the automatic choice for M = 1; 8: M <= 16, K % 128 == 0,
+ * K <= 4096, bfloat16/float16 x read as given, MFMA on the exact integer codes with the group
+ * scale applied in fp32 -- the automatic choice for 2 <= M <= 16 where it applies). For tuning
+ * and tests; results agree to rounding. */
 #define QL_W4A16_CFG_SHIFT 8
 #define QL_W4A16_CFG_MASK (0xF << QL_W4A16_CFG_SHIFT)
 #define QL_W4A16_CFG(c) (((c) + 1) << QL_W4A16_CFG_SHIFT)

@@ -89,11 +89,20 @@ def test_w4a16_argument_checks(lib):
     assert "null" in _err(lib)
     assert f(1, 2, ctypes.c_void_p(8), None, ctypes.c_void_p(16), ctypes.c_void_p(16), None, ctypes.c_void_p(16),
              4, 64, 64, 0, 0, None, 0, None) == QL_ERR_ALIGN
-    # forced kernel configurations (flags bits 8-11 = configuration + 1): 0-6 exist; the 256 x 256
+    # forced kernel configurations (flags bits 8-11 = configuration + 1): 0-8 exist; the 256 x 256
     # configurations 4-6 need K % 64 == 0 and whole tiles
     cfg = lambda c: (c + 1) << 8  # noqa: E731
-    assert f(2, 2, None, None, None, None, None, None, 0, 64, 64, 0, cfg(8), None, 0, None) == QL_ERR_ARG
-    assert "configuration 8 does not exist" in _err(lib)
+    assert f(2, 2, None, None, None, None, None, None, 0, 64, 64, 0, cfg(9), None, 0, None) == QL_ERR_ARG
+    assert "configuration 9 does not exist" in _err(lib)
+    # configuration 8 (MFMA, M <= 16): 16-bit x, K % 128 == 0, K <= 4096, no K split
+    assert f(2, 2, None, None, None, None, None, None, 0, 64, 128, 0, cfg(8), None, 0, None) == QL_OK
+    assert f(0, 2, None, None, None, None, None, None, 0, 64, 128, 0, cfg(8), None, 0, None) == QL_ERR_SHAPE
+    assert f(2, 2, None, None, None, None, None, None, 17, 64, 128, 0, cfg(8), None, 0, None) == QL_ERR_SHAPE
+    assert f(2, 2, None, None, None, None, None, None, 1, 64, 96, 0, cfg(8), None, 0, None) == QL_ERR_SHAPE
+    assert f(2, 2, None, None, None, None, None, None, 1, 64, 4224, 0, cfg(8), None, 0, None) == QL_ERR_SHAPE
+    assert "K % 128 == 0" in _err(lib)
+    assert f(2, 2, None, None, None, None, None, None, 0, 64, 128, 2, cfg(8), None, 0, None) == QL_ERR_ARG
+    assert "no K split" in _err(lib)
     # configuration 7 (VALU, M <= 4): 16-bit x, K <= 8192
     assert f(0, 2, None, None, None, None, None, None, 0, 64, 64, 0, cfg(7), None, 0, None) == QL_ERR_SHAPE
     assert f(2, 2, None, None, None, None, None, None, 5, 64, 64, 0, cfg(7), None, 0, None) == QL_ERR_SHAPE

@@ -311,7 +311,7 @@ def test_w4a16_gemv_exact_on_integer_grid():
 def test_w4a16_gemv_16bit_out_gelu_and_row_scale(out_dtype):
     """16-bit outputs (1 ulp + gate), the fused GELU (1 ulp of the exact GELU of the plain output),
     and fp16 x staged by rows_to_f16 with its row scale, through configuration 7 and the automatic
-    choice (which takes configuration 7 for M <= 4)."""
+    choice."""
     from comfy_ui_gfx906_tools_amd import _lib as L
     M, N, K = 3, 300, 3072
     x, wq, ws = seeded_linear(M, N, K, seed=51)
@@ -332,4 +332,76 @@ def test_w4a16_gemv_16bit_out_gelu_and_row_scale(out_dtype):
     x16, rs = L.rows_to_f16(x.to(DEV))
     y = to_np_f32(L.w4a16_gemm(x16, wq.to(DEV), ws.to(DEV), bias.to(DEV), out_dtype=out_dtype, row_scale=rs,
                                config=GEMV_CFG))
+    assert (np.abs(y - ref_r) <= ulp + 2e-4 * np.abs(ref).max()).all()
+
+
+SKINNY_CFG = 8
+
+
+@pytest.mark.parametrize("M", [1, 5, 16])
+@pytest.mark.parametrize("N,K", [(1, 128), (33, 256), (100, 4096), (257, 3072), (64, 384)])
+@pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
+def test_w4a16_skinny_vs_oracle(M, N, K, xdt):
+    """Configuration 8 (M <= 16, MFMA on exact codes, K split over 8 waves): ragged N (columns past
+    N in the last workgroup), K slices of 4 to 16 groups with idle waves (K = 128: one slice), bias,
+    fp32 out; deterministic and within 2e-4 of the fp64 oracle (exact products, fp32 sums)."""
+    print(f"case skinny M={M} N={N} K={K} x={xdt}", flush=True)
+    x, wq, ws = seeded_linear(M, N, K, seed=11 * M + N + K, x_dtype=xdt)
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(M))
+    y1 = _run_cfg(x, wq, ws, bias, cfg=SKINNY_CFG)
+    y2 = _run_cfg(x, wq, ws, bias, cfg=SKINNY_CFG)
+    assert torch.equal(y1, y2), "not deterministic"
+    ref = orc.w4a16_reference(to_np_f32(x), wq.numpy(), ws.numpy(), bias.numpy())
+    err = rel_max_err(to_np_f32(y1), ref)
+    assert err <= 2e-4, f"max rel err {err:.3e}"
+
+
+@pytest.mark.parametrize("M,K,msg", [(17, 256, "M <= 16"), (4, 160, "K % 128 == 0"), (4, 8192, "K <= 4096")])
+def test_w4a16_skinny_rejects_unsupported_shapes(M, K, msg):
+    x, wq, ws = seeded_linear(M, 8, K, seed=3)
+    with pytest.raises(RuntimeError, match=msg):
+        _run_cfg(x, wq, ws, cfg=SKINNY_CFG)
+
+
+def test_w4a16_skinny_exact_on_integer_grid():
+    """Integer x, codes in [-8, 7], power-of-two scales: every partial sum is exact in fp32, so the
+    MFMA kernel must equal the fp64 oracle exactly (both dtypes, all 16 rows)."""
+    M, N, K = 16, 70, 1024
+    g = np.random.default_rng(43)
+    codes = g.integers(-8, 8, (N, K))
+    nib = (codes & 0xF).astype(np.uint8)
+    packed = (nib[:, 0::2] | (nib[:, 1::2] << 4)).view(np.int8)
+    scale = (2.0 ** g.integers(-6, 0, (N, K // 32))).astype(np.float32)
+    for xdt in (torch.bfloat16, torch.float16):
+        x = torch.from_numpy(g.integers(-4, 5, (M, K)).astype(np.float32)).to(xdt)
+        y = to_np_f32(_run_cfg(x, torch.from_numpy(packed), torch.from_numpy(scale), cfg=SKINNY_CFG))
+        ref = orc.w4a16_reference(to_np_f32(x), packed, scale)
+        assert np.array_equal(y.astype(np.float64), ref), f"{xdt}: max abs diff {np.abs(y - ref).max()}"
+
+
+@pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16])
+def test_w4a16_skinny_16bit_out_gelu_and_row_scale(out_dtype):
+    """16-bit outputs (1 ulp + gate), the fused GELU (1 ulp of the exact GELU of the plain output),
+    and fp16 x staged by rows_to_f16 with its row scale, through configuration 8 and the automatic
+    choice (which takes configuration 8 for 4 < M <= 16)."""
+    from comfy_ui_gfx906_tools_amd import _lib as L
+    M, N, K = 12, 300, 3072
+    x, wq, ws = seeded_linear(M, N, K, seed=53)
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(7)).to(out_dtype)
+    ref = orc.w4a16_reference(to_np_f32(x), wq.numpy(), ws.numpy(), to_np_f32(bias)).astype(np.float32)
+    name = "bfloat16" if out_dtype == torch.bfloat16 else "float16"
+    ref_r = orc.round_to_dtype(ref, name)
+    ulp = bf16_ulp(ref_r) if out_dtype == torch.bfloat16 else f16_ulp(ref_r)
+    for cfg in (SKINNY_CFG, None):
+        y = to_np_f32(_run_cfg(x, wq, ws, bias, out_dtype=out_dtype, cfg=cfg))
+        assert (np.abs(y - ref_r) <= ulp + 2e-4 * np.abs(ref).max()).all()
+    plain = _run_cfg(x, wq, ws, bias, out_dtype=out_dtype, cfg=SKINNY_CFG)
+    fused = L.w4a16_gemm(x.to(DEV), wq.to(DEV), ws.to(DEV), bias.to(DEV), out_dtype=out_dtype, config=SKINNY_CFG,
+                         gelu=True)
+    e = orc.round_to_dtype(_gelu_tanh_f64(to_np_f32(plain)).astype(np.float32), name)
+    ue = bf16_ulp(e) if out_dtype == torch.bfloat16 else f16_ulp(e)
+    assert (np.abs(to_np_f32(fused) - e) <= ue).all()
+    x16, rs = L.rows_to_f16(x.to(DEV))
+    y = to_np_f32(L.w4a16_gemm(x16, wq.to(DEV), ws.to(DEV), bias.to(DEV), out_dtype=out_dtype, row_scale=rs,
+                               config=SKINNY_CFG))
     assert (np.abs(y - ref_r) <= ulp + 2e-4 * np.abs(ref).max()).all()
