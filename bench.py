@@ -11,6 +11,13 @@ around its launches, the parity gate of this same run, and the CPU baseline (the
 dequant-then-matmul path on the host cores).
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
+
+`--workload c3` and `--workload c4` instead measure the other BASELINE configurations (one JSON
+line each, not the driver's line): C3 = the W8A8 linear 3072 -> 21504 at M = 4608 (per-token int8
+quantize + int8 GEMM, bf16 out) against the int8 MFMA peak; C4 = the skinny-M sweep (W4A16 at
+K = 4096, N = 10240 for M in {1, 4, 16, 64, 256}, plus 3072 -> 18432 at M = 1) against the HBM
+peak, with 12 weight copies in rotation (more than the 256 MB last-level cache) and the calls
+replayed back to back from a HIP graph.
 """
 from __future__ import annotations
 
@@ -33,6 +40,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-repeats", type=int, default=3)
+    ap.add_argument("--workload", choices=["c2", "c3", "c4"], default="c2")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy three times (reference kernel for the "
                          "FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -93,6 +101,12 @@ def main():
         sys.exit(2)
     if args.calibrate_copy:
         calibrate_copy()
+        return
+    if args.workload == "c3":
+        bench_c3(args)
+        return
+    if args.workload == "c4":
+        bench_c4(args)
         return
     import numpy as np
     import torch
@@ -202,6 +216,133 @@ def main():
         cb.pop("_check", None)
         out["cpu_baseline"] = cb
     print(json.dumps(out), flush=True)
+
+
+PEAK_INT8_TOPS = 5000.0  # MI355X dense int8 MFMA, AMD spec
+PEAK_HBM_GBS = 8000.0    # MI355X HBM3E
+
+
+def bench_c3(args):
+    """C3: y = W8A8(x) for the fused single-stream linear 3072 -> 21504 at M = 4608. One step =
+    per-token int8 quantize of the bf16 activations + the int8 GEMM with the per-token x
+    per-channel epilogue, bf16 out. Parity: the int32 accumulators equal a float64 matmul of the
+    same codes (exact), and the bf16 output equals torch's fp32 composition in the same order."""
+    import numpy as np
+    import torch
+    sys.path.insert(0, HERE)
+    from comfy_ui_gfx906_tools_amd import _lib
+    M, K, N = 4608, 3072, 21504
+    torch.cuda.set_device(0)
+    _lib.load_library()
+    g = torch.Generator(device="cuda").manual_seed(2)
+    x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+    w = torch.randn(N, K, device="cuda", generator=g) * 0.02
+    wq, sw = _lib.quantize_int8_per_token(w)  # per-output-channel weight rule (same kernel)
+    del w
+    xq, sx = _lib.quantize_int8_per_token(x)
+    acc = _lib.w8a8_gemm(xq, None, wq, None, out_dtype=torch.int32)
+    exact = bool(torch.equal(acc.double(), xq.double() @ wq.double().t()))
+    y = _lib.w8a8_gemm(xq, sx, wq, sw, out_dtype=torch.bfloat16)
+    same = bool(torch.equal(y, (acc.float() * (sx[:, None] * sw[None, :])).to(torch.bfloat16)))
+    del acc
+    ev = []
+
+    def step(record):
+        q, s = _lib.quantize_int8_per_token(x)
+        if record:
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+        out = _lib.w8a8_gemm(q, s, wq, sw, out_dtype=torch.bfloat16)
+        if record:
+            e1.record()
+            ev.append((e0, e1))
+        return out
+
+    for _ in range(args.warmup):
+        step(False)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for _ in range(args.steps):
+        step(True)
+    torch.cuda.synchronize()
+    el = (time.perf_counter() - t0) / args.steps
+    gemm_ms = sum(a.elapsed_time(b) for a, b in ev) / len(ev)
+    ops = 2.0 * M * N * K
+    out = {"metric": "W8A8 GEMM TOP/s at the C3 shape (quantize + GEMM per step)", "value": round(ops / el / 1e12, 2),
+           "unit": "TOP/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(el * 1e3, 4),
+           "higher_is_better": True, "dtype": "int8 (int32 accumulate)", "data": "synthetic",
+           "config": {"workload": "C3 W8A8 linear 3072->21504, M=4608, per-token x per-channel, bf16 out"},
+           "roofline": {"bound": "mfma", "achieved": round(ops / (gemm_ms * 1e-3) / 1e12, 2), "peak": PEAK_INT8_TOPS,
+                        "unit": "TOP/s", "frac": round(ops / (gemm_ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4),
+                        "kernel": "w8a8_tile256_kernel", "avg_launch_ms": round(gemm_ms, 4)},
+           "parity": {"int32_accumulators_exact": exact, "bf16_epilogue_exact": same, "pass": exact and same}}
+    if not args.no_cpu_baseline:
+        # the oracle's exact integer matmul (int64 numpy) on a bounded sample of rows, scaled
+        from oracle import qlinear_oracle as orc
+        rows = 64
+        a = xq[:rows].cpu().numpy()
+        b = wq.cpu().numpy()
+        t0 = time.perf_counter()
+        orc.int8_matmul_exact(a, b)
+        dt = time.perf_counter() - t0
+        out["cpu_baseline"] = {"value": round(2.0 * rows * N * K / dt / 1e12, 5), "unit": "TOP/s", "cores": 1,
+                               "kind": "port", "sample": f"oracle int8_matmul_exact on {rows} of {M} rows "
+                                                          f"(int64 numpy), {dt:.2f} s"}
+    print(json.dumps(out), flush=True)
+
+
+def bench_c4(args):
+    """C4: W4A16 at skinny M, HBM-bound. For each shape, 12 weight copies (> MALL) are rotated
+    through 48 calls captured in one HIP graph, replayed back to back; the time per call is the
+    replay time / 48 (median of 5 replays). Bytes = packed weights + fp32 scales + x + y."""
+    import statistics
+    import torch
+    sys.path.insert(0, HERE)
+    from comfy_ui_gfx906_tools_amd import _lib, ops
+    torch.cuda.set_device(0)
+    _lib.load_library()
+    shapes = [(1, 4096, 10240), (4, 4096, 10240), (16, 4096, 10240), (64, 4096, 10240), (256, 4096, 10240),
+              (1, 3072, 18432)]
+    side = torch.cuda.Stream()
+    res = []
+    for M, K, N in shapes:
+        g = torch.Generator(device="cuda").manual_seed(4)
+        x = torch.randn(M, K, device="cuda", generator=g).to(torch.bfloat16)
+        b = (torch.randn(N, device="cuda", generator=g) * 0.02).to(torch.bfloat16)
+        ws = []
+        for _ in range(12):
+            w = torch.randn(N, K, device="cuda", generator=g) * 0.02
+            ws.append(ops.quantize_pack_int4(w))
+        del w
+        with torch.cuda.stream(side):
+            for q, s in ws:  # eager calls on the capture stream first: its workspace exists before capture
+                y = _lib.w4a16_gemm(x, q, s, b, out_dtype=torch.bfloat16)
+        side.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            for i in range(48):
+                q, s = ws[i % 12]
+                y = _lib.w4a16_gemm(x, q, s, b, out_dtype=torch.bfloat16)
+        graph.replay()
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(5):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            graph.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1) * 1e3 / 48)
+        us = statistics.median(times)
+        nbytes = N * K / 2 + N * (K // 32) * 4 + M * K * 2 + M * N * 2
+        res.append({"M": M, "K": K, "N": N, "us_per_call": round(us, 2), "GB_s": round(nbytes / us / 1e3, 1),
+                    "hbm_frac": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4)})
+        del graph, ws, y
+        torch.cuda.empty_cache()
+    print(json.dumps({"metric": "W4A16 skinny-M GB/s vs 8 TB/s HBM (C4)", "unit": "GB/s", "n_gpus": 1,
+                      "dtype": "int4 weights, bf16 activations", "data": "synthetic",
+                      "timing": "HIP graph of 48 calls over 12 weight copies, replayed back to back",
+                      "results": res}), flush=True)
 
 
 def dequant_fp32(w_q4, w_scale):
