@@ -7,7 +7,7 @@
 //   scalar-divisor path on GPU and csrc/int4_gemm_scaled.hip:210-211). One thread per block.
 // quantize_int8_per_token: s = max(amax(row), 1e-8) * fl(1/127),
 //   q = clamp(rint(x / s), -127, 127) (csrc/int8_gemm.hip:215-246, block widened to the row).
-//   One 256-thread workgroup per row.
+//   One 256-thread workgroup per row; rows of K % 8 == 0 up to 16384 stay in registers.
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -95,6 +95,76 @@ __global__ __launch_bounds__(kQThreads) void quantize_int8_row_kernel(const void
   }
 }
 
+// Same rule, for K % 8 == 0 and K <= 8 * kQThreads * kQ8Vec: each thread reads its 8-element
+// vectors once (16-byte loads for 16-bit x) and keeps them in registers between the row maximum
+// and the quantize pass; 8 codes leave as one 8-byte store.
+constexpr int kQ8Vec = 8;
+template <int DT>
+__global__ __launch_bounds__(kQThreads) void quantize_int8_row_vec_kernel(const void* __restrict__ x,
+                                                                          int8_t* __restrict__ q,
+                                                                          float* __restrict__ scale, int K) {
+  __shared__ float red[kQThreads / kWave];
+  const int row = blockIdx.x;
+  const size_t base = (size_t)row * K;
+  const int nv = K / 8;
+  float v[kQ8Vec][8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int i = 0; i < kQ8Vec; ++i) {
+    const int vi = threadIdx.x + i * kQThreads;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[i][e] = 0.0f;
+    if (vi < nv) {
+      if constexpr (DT == kF32) {
+        const u32x4 lo = *(const u32x4*)((const float*)x + base + 8 * vi);
+        const u32x4 hi = *(const u32x4*)((const float*)x + base + 8 * vi + 4);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t a = lo[e], b = hi[e];
+          v[i][e] = __builtin_bit_cast(float, a);
+          v[i][4 + e] = __builtin_bit_cast(float, b);
+        }
+      } else {
+        const u32x4 w = *(const u32x4*)((const uint16_t*)x + base + 8 * vi);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t lo = w[e] & 0xFFFFu, hi = w[e] >> 16;
+          v[i][2 * e] = DT == kBF16 ? bf16_bits_to_f32(lo) : f16_bits_to_f32(lo);
+          v[i][2 * e + 1] = DT == kBF16 ? bf16_bits_to_f32(hi) : f16_bits_to_f32(hi);
+        }
+      }
+    }
+#pragma unroll
+    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[i][e]));
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, kWave));
+  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+  __syncthreads();
+  amax = red[0];
+#pragma unroll
+  for (int w = 1; w < kQThreads / kWave; ++w) amax = fmaxf(amax, red[w]);
+  const float s = __fmul_rn(fmaxf(amax, 1e-8f), 1.0f / 127.0f);
+  if (threadIdx.x == 0) scale[row] = s;
+#pragma unroll
+  for (int i = 0; i < kQ8Vec; ++i) {
+    const int vi = threadIdx.x + i * kQThreads;
+    if (vi < nv) {
+      uint32_t lo = 0, hi = 0;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t c = (uint32_t)(int)fminf(fmaxf(rintf(__fdiv_rn(v[i][e], s)), -127.0f), 127.0f) & 0xFFu;
+        if (e < 4)
+          lo |= c << (8 * e);
+        else
+          hi |= c << (8 * (e - 4));
+      }
+      typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+      *(u32x2*)(q + base + 8 * vi) = u32x2{lo, hi};
+    }
+  }
+}
+
 }  // namespace
 
 hipError_t quantize_int4_launch(int dtype, int rule, const void* x, void* packed, float* scale,
@@ -121,6 +191,22 @@ hipError_t quantize_int4_launch(int dtype, int rule, const void* x, void* packed
 hipError_t quantize_int8_per_token_launch(int dtype, const void* x, int8_t* q, float* scale, int64_t M,
                                           int64_t K, hipStream_t stream) {
   const dim3 grid((unsigned)M);
+  // 16-byte loads need 16-byte aligned rows: K % 8 == 0 and an aligned base (checked by the caller)
+  if (K % 8 == 0 && K <= 8 * kQThreads * kQ8Vec && ((uintptr_t)x & 15) == 0 && ((uintptr_t)q & 7) == 0) {
+    switch (dtype) {
+      case kF32:
+        hipLaunchKernelGGL(quantize_int8_row_vec_kernel<kF32>, grid, dim3(kQThreads), 0, stream, x, q, scale, (int)K);
+        break;
+      case kF16:
+        hipLaunchKernelGGL(quantize_int8_row_vec_kernel<kF16>, grid, dim3(kQThreads), 0, stream, x, q, scale, (int)K);
+        break;
+      default:
+        hipLaunchKernelGGL(quantize_int8_row_vec_kernel<kBF16>, grid, dim3(kQThreads), 0, stream, x, q, scale,
+                           (int)K);
+        break;
+    }
+    return hipGetLastError();
+  }
   switch (dtype) {
     case kF32:
       hipLaunchKernelGGL(quantize_int8_row_kernel<kF32>, grid, dim3(kQThreads), 0, stream, x, q, scale, (int)K);

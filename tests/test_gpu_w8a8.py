@@ -17,8 +17,11 @@ def _lib():
     return _lib
 
 
+# K % 8 == 0 and K <= 16384 take the register-resident vector kernel; (5, 1004) and (3, 16392)
+# the element-wise one
 @pytest.mark.parametrize("M,K,dt", [(1, 64, torch.bfloat16), (7, 3072, torch.bfloat16), (300, 1000, torch.float16),
-                                    (64, 4096, torch.float32)])
+                                    (64, 4096, torch.float32), (5, 1004, torch.float16), (3, 16392, torch.bfloat16),
+                                    (2, 16384, torch.float32)])
 def test_quantize_int8_per_token_matches_oracle(M, K, dt):
     print(f"case quant8 M={M} K={K} {dt}", flush=True)
     g = torch.Generator().manual_seed(M + K)
