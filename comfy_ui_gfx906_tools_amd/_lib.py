@@ -50,6 +50,7 @@ SIGNATURES = {
     "qlinear_w4a16_auto_splits": (_c_int, [_c_i64, _c_i64, _c_i64, _c_int]),
     "qlinear_quantize_int4": (_c_int, [_c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
     "qlinear_quantize_int8_per_token": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
+    "qlinear_repack_q4_0": (_c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
     "qlinear_w8a8_gemm": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp]),
 }
 
@@ -225,6 +226,26 @@ def quantize_int4(x: torch.Tensor, rule: int = RULE_RECIP) -> tuple[torch.Tensor
         rc = lib.qlinear_quantize_int4(_DTYPE_CODE[x.dtype], rule, x.data_ptr(), packed.data_ptr(), scale.data_ptr(),
                                        rows, K, _stream_ptr(x.device))
     _check(rc, "quantize_int4")
+    return packed, scale
+
+
+def repack_q4_0(raw: torch.Tensor, out_features: int, in_features: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """ggml Q4_0 bytes of a [out_features, in_features] weight (device tensor) -> (int8
+    [out, in/2], fp32 [out, in/32]) in the native layout, by the HIP kernel."""
+    lib = load_library()
+    raw = _dev_tensor(raw, "raw").reshape(-1)
+    nbytes = raw.numel() * raw.element_size()
+    if in_features % 32 != 0 or nbytes != out_features * (in_features // 32) * 18:
+        raise RuntimeError(f"Q4_0 data of {nbytes} bytes does not hold a [{out_features}, {in_features}] weight "
+                           f"(expected {out_features * (in_features // 32) * 18} bytes, in_features % 32 == 0)")
+    packed = torch.empty((out_features, in_features // 2), dtype=torch.int8, device=raw.device)
+    scale = torch.empty((out_features, in_features // 32), dtype=torch.float32, device=raw.device)
+    if out_features == 0:
+        return packed, scale
+    with torch.cuda.device(raw.device):
+        rc = lib.qlinear_repack_q4_0(raw.data_ptr(), packed.data_ptr(), scale.data_ptr(), out_features, in_features,
+                                     _stream_ptr(raw.device))
+    _check(rc, "repack_q4_0")
     return packed, scale
 
 

@@ -366,6 +366,19 @@ int qlinear_quantize_int4(int x_dtype, int rule, const void* x, void* packed, fl
   return ok();
 }
 
+int qlinear_repack_q4_0(const void* raw, int8_t* packed, float* scale, int64_t rows, int64_t K, void* stream) {
+  if (rows < 0 || K < 32 || K % 32 != 0)
+    return fail(QL_ERR_SHAPE, "Q4_0 weight must be [rows, K] with K %% 32 == 0, got [%lld, %lld]", (long long)rows,
+                (long long)K);
+  if (rows == 0) return ok();
+  if (!raw || !packed || !scale) return fail(QL_ERR_ARG, "null raw / packed / scale pointer");
+  if (((uintptr_t)raw & 1) || !aligned16(packed) || ((uintptr_t)scale & 3))
+    return fail(QL_ERR_ALIGN, "raw must be 2-byte, packed 16-byte and scale 4-byte aligned");
+  const hipError_t e = repack_q4_0_launch(raw, packed, scale, rows * (K / 32), (hipStream_t)stream);
+  if (e != hipSuccess) return fail(QL_ERR_LAUNCH, "repack_q4_0 launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
 int qlinear_quantize_int8_per_token(int x_dtype, const void* x, int8_t* q, float* scale, int64_t M, int64_t K,
                                     void* stream) {
   if (x_dtype != QL_F32 && x_dtype != QL_F16 && x_dtype != QL_BF16)

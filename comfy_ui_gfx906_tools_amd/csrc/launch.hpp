@@ -80,6 +80,7 @@ hipError_t w8a8_tile256_launch(const W8A8Params& p, hipStream_t stream);
 
 hipError_t quantize_int4_launch(int dtype, int rule, const void* x, void* packed, float* scale,
                                 int64_t rows, int64_t K, hipStream_t stream);
+hipError_t repack_q4_0_launch(const void* raw, void* packed, float* scale, int64_t blocks, hipStream_t stream);
 hipError_t quantize_int8_per_token_launch(int dtype, const void* x, int8_t* q, float* scale,
                                           int64_t M, int64_t K, hipStream_t stream);
 

@@ -8,6 +8,7 @@
 // quantize_int8_per_token: s = max(amax(row), 1e-8) * fl(1/127),
 //   q = clamp(rint(x / s), -127, 127) (csrc/int8_gemm.hip:215-246, block widened to the row).
 //   One 256-thread workgroup per row; rows of K % 8 == 0 up to 16384 stay in registers.
+// repack_q4_0: lossless ggml Q4_0 -> native layout (nodes/ComfyUI-Gfx906Int4/ops.py:129-164).
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -165,7 +166,42 @@ __global__ __launch_bounds__(kQThreads) void quantize_int8_row_vec_kernel(const 
   }
 }
 
+// ggml Q4_0 -> native layout, one thread per 32-element block: the 18-byte block (fp16 d, then
+// 16 bytes whose byte i holds elements i (low nibble) and i + 16 (high nibble) as q + 8) becomes
+// 16 bytes of two's-complement nibbles in element order (byte j = elements 2j | 2j+1 << 4) and
+// the fp32 scale d (exact widening). Blocks are only 2-byte aligned: read as 9 halfwords.
+__global__ __launch_bounds__(kQThreads) void repack_q4_0_kernel(const uint16_t* __restrict__ raw,
+                                                                u32x4* __restrict__ packed,
+                                                                float* __restrict__ scale, long long blocks) {
+  const long long b = (long long)blockIdx.x * kQThreads + threadIdx.x;
+  if (b >= blocks) return;
+  const uint16_t* src = raw + b * 9;
+  uint32_t e[32];
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const uint32_t hw = src[1 + i];  // bytes 2i, 2i+1 of the quants
+#pragma unroll
+    for (int k = 0; k < 2; ++k) {
+      const uint32_t byte = (hw >> (8 * k)) & 0xFFu;
+      e[2 * i + k] = ((byte & 0xFu) - 8u) & 0xFu;          // element 2i + k
+      e[2 * i + k + 16] = (((byte >> 4) & 0xFu) - 8u) & 0xFu;  // element 2i + k + 16
+    }
+  }
+  u32x4 out = {0u, 0u, 0u, 0u};
+#pragma unroll
+  for (int j = 0; j < 32; ++j) out[j / 8] |= e[j] << (4 * (j % 8));
+  packed[b] = out;
+  scale[b] = f16_bits_to_f32(src[0]);
+}
+
 }  // namespace
+
+hipError_t repack_q4_0_launch(const void* raw, void* packed, float* scale, int64_t blocks, hipStream_t stream) {
+  const dim3 grid((unsigned)((blocks + kQThreads - 1) / kQThreads));
+  hipLaunchKernelGGL(repack_q4_0_kernel, grid, dim3(kQThreads), 0, stream, (const uint16_t*)raw, (u32x4*)packed, scale,
+                     (long long)blocks);
+  return hipGetLastError();
+}
 
 hipError_t quantize_int4_launch(int dtype, int rule, const void* x, void* packed, float* scale,
                                 int64_t rows, int64_t K, hipStream_t stream) {

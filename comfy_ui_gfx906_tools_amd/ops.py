@@ -116,7 +116,10 @@ def quantize_pack_int4(t: torch.Tensor, block: int = BLOCK):
 
 def repack_q4_0_native(raw_bytes: torch.Tensor, out_features: int, in_features: int, block: int = BLOCK):
     """Lossless ggml Q4_0 (18-byte blocks: fp16 d, 16 bytes of offset-binary nibbles in
-    split-half order) -> native two's-complement interleaved int4 + fp32 scales (ops.py:129-164)."""
+    split-half order) -> native two's-complement interleaved int4 + fp32 scales (ops.py:129-164).
+    Device tensors go through the HIP repack kernel; CPU tensors through the torch expression."""
+    if raw_bytes.device.type == "cuda" and block == BLOCK:
+        return _lib.repack_q4_0(raw_bytes, out_features, in_features)
     n_blocks = out_features * (in_features // block)
     blocks = raw_bytes.reshape(-1).view(torch.uint8).reshape(n_blocks, 18)
     scale = blocks[:, :2].contiguous().view(torch.float16).reshape(n_blocks).float()

@@ -121,6 +121,16 @@ int qlinear_quantize_int4(int x_dtype, int rule, const void* x, void* packed, fl
                           int64_t rows, int64_t K, void* stream);
 
 /* ---------------------------------------------------------------------------------------
+ * Lossless ggml Q4_0 -> native layout of a weight [rows, K]: rows * K/32 blocks of 18 bytes
+ * (fp16 d, then 16 bytes whose byte i holds elements i and i + 16 as offset-binary nibbles)
+ * become w_q4 [rows, K/2] (two's-complement nibbles, element 2j in the low nibble of byte j)
+ * and w_scale [rows, K/32] fp32 = d. Replaces repack_q4_0_native (ops.py:129-164) for
+ * device-resident GGUF tensors. raw 2-byte aligned, packed 16-byte aligned.
+ * ------------------------------------------------------------------------------------- */
+int qlinear_repack_q4_0(const void* raw, int8_t* packed, float* scale, int64_t rows, int64_t K,
+                        void* stream);
+
+/* ---------------------------------------------------------------------------------------
  * Per-token int8 quantize of activations x[M,K] (fp32/fp16/bf16):
  *   s[m] = max(amax(row m), 1e-8) * (1/127); q = clamp(rint(x / s), -127, 127)
  * The reference's int8 rule (csrc/int8_gemm.hip:215-246, quantize_int8_dispatch :280) with

@@ -121,6 +121,12 @@ def test_quantizer_and_w8a8_argument_checks(lib):
     assert lib.qlinear_quantize_int4(2, 0, None, None, None, 4, 40, None) == QL_ERR_SHAPE
     assert lib.qlinear_quantize_int4(3, 0, None, None, None, 4, 64, None) == QL_ERR_DTYPE
     assert lib.qlinear_quantize_int4(2, 0, None, None, None, 0, 64, None) == QL_OK
+    # Q4_0 repack: K % 32, null pointers, a source that is not 2-byte aligned
+    assert lib.qlinear_repack_q4_0(None, None, None, 4, 48, None) == QL_ERR_SHAPE
+    assert lib.qlinear_repack_q4_0(None, None, None, 0, 64, None) == QL_OK
+    assert lib.qlinear_repack_q4_0(None, None, None, 4, 64, None) == QL_ERR_ARG
+    assert lib.qlinear_repack_q4_0(ctypes.c_void_p(17), ctypes.c_void_p(256), ctypes.c_void_p(512), 4, 64,
+                                   None) == QL_ERR_ALIGN
     assert lib.qlinear_quantize_int8_per_token(3, None, None, None, 4, 64, None) == QL_ERR_DTYPE
     assert lib.qlinear_quantize_int8_per_token(2, None, None, None, 4, 64, None) == QL_ERR_ARG
     assert lib.qlinear_w8a8_gemm(2, None, None, None, None, None, None, 4, 64, 96, None) == QL_ERR_SHAPE

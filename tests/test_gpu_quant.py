@@ -56,3 +56,42 @@ def test_quantize_pack_int4_gpu_equals_reference_torch_on_gpu():
         p1, s1 = _lib().quantize_int4(w, 1)
         pytest.fail(f"scale mismatch: torch-GPU == rule0? {torch.equal(s0, s_ref)}; == rule1? {torch.equal(s1, s_ref)}")
     assert torch.equal(p, p_ref)
+
+
+@pytest.mark.parametrize("out_f,in_f,offset", [(1, 32, 0), (5, 96, 2), (300, 4096, 0), (7, 3072, 2)])
+def test_repack_q4_0_matches_oracle(out_f, in_f, offset):
+    """HIP Q4_0 -> native repack (ops.py:129-164): bit-exact against the oracle's restatement, and
+    dequantized equal to the ggml Q4_0 definition; fp16 d of every class (zero, -0, subnormal,
+    max), a block with every nibble 0 (code -8), and a source only 2-byte aligned (offset 2)."""
+    print(f"case q4_0 {out_f}x{in_f} offset={offset}", flush=True)
+    rng = np.random.default_rng(out_f + in_f)
+    n = out_f * in_f // 32
+    d = (rng.standard_normal(n) * 0.01).astype(np.float16)
+    special = np.array([0.0, -0.0, 6e-8, 65504.0, -2.0 ** -14], dtype=np.float16)
+    d[: min(n, len(special))] = special[: min(n, len(special))]
+    qs = rng.integers(0, 256, (n, 16)).astype(np.uint8)
+    qs[-1] = 0  # every element at code -8
+    raw = np.concatenate([d.view(np.uint8).reshape(n, 2), qs], axis=1).reshape(-1)
+    buf = torch.zeros(raw.size + offset, dtype=torch.uint8)
+    buf[offset:] = torch.from_numpy(raw)
+    dev = buf.to(DEV)[offset:]
+    packed, scale = _lib().repack_q4_0(dev, out_f, in_f)
+    p_ref, s_ref = orc.repack_q4_0_native(raw, out_f, in_f)
+    assert np.array_equal(packed.cpu().numpy(), p_ref)
+    assert np.array_equal(scale.cpu().numpy().view(np.uint32), s_ref.view(np.uint32))
+    deq = orc.dequant_int4(packed.cpu().numpy(), scale.cpu().numpy())
+    assert np.array_equal(deq, orc.ggml_q4_0_dequant(raw, out_f, in_f))
+
+
+def test_repack_q4_0_through_ops_on_device():
+    """ops.repack_q4_0_native takes the HIP kernel for device tensors and returns the same as on CPU."""
+    from comfy_ui_gfx906_tools_amd import ops
+    rng = np.random.default_rng(9)
+    out_f, in_f = 16, 256
+    n = out_f * in_f // 32
+    d = (rng.standard_normal(n) * 0.01).astype(np.float16)
+    raw = np.concatenate([d.view(np.uint8).reshape(n, 2), rng.integers(0, 256, (n, 16)).astype(np.uint8)], axis=1)
+    t = torch.from_numpy(raw.reshape(-1))
+    p_cpu, s_cpu = ops.repack_q4_0_native(t, out_f, in_f)
+    p_dev, s_dev = ops.repack_q4_0_native(t.to(DEV), out_f, in_f)
+    assert p_dev.is_cuda and torch.equal(p_dev.cpu(), p_cpu) and torch.equal(s_dev.cpu(), s_cpu)
