@@ -40,7 +40,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-repeats", type=int, default=3)
-    ap.add_argument("--workload", choices=["c2", "c3", "c4"], default="c2")
+    ap.add_argument("--workload", choices=["c2", "c3", "c4", "c5"], default="c2")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy three times (reference kernel for the "
                          "FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -107,6 +107,9 @@ def main():
         return
     if args.workload == "c4":
         bench_c4(args)
+        return
+    if args.workload == "c5":
+        bench_c5(args)
         return
     import numpy as np
     import torch
@@ -343,6 +346,113 @@ def bench_c4(args):
                       "dtype": "int4 weights, bf16 activations", "data": "synthetic",
                       "timing": "HIP graph of 48 calls over 12 weight copies, replayed back to back",
                       "results": res}), flush=True)
+
+
+def bench_c5(args):
+    """C5: one denoise step of the 12B Flux-style DiT (19 double + 38 single blocks, hidden 3072,
+    4096 image + 512 text tokens, batch 1), random init, every Linear on the W4A16 engine,
+    attention on SDPA. Timed: `steps` whole forward steps after `warmup`, bracketed by
+    synchronizations. Parity: double block 0 and single block 0 on the GPU against the same
+    blocks in fp32 on the host (weights = the dequantized int4 codes, same input activations);
+    the host time of those two blocks, scaled by the block counts, is the CPU baseline."""
+    import numpy as np
+    import torch
+    sys.path.insert(0, HERE)
+    from comfy_ui_gfx906_tools_amd import _lib, flux_dit as fd
+    torch.cuda.set_device(0)
+    _lib.load_library()
+    cfg = fd.FluxDiTConfig.flux12b()
+    n_side, n_txt = 64, 512
+    t0 = time.perf_counter()
+    with torch.no_grad():
+        model = fd.FluxDiT(cfg, device="cuda", dtype=torch.bfloat16)
+        fd.init_random_(model, seed=4)
+        torch.cuda.synchronize()
+        t_init = time.perf_counter() - t0
+        inp = fd.synthetic_inputs(cfg, n_side, n_txt, seed=4, device="cuda")
+        n_params = sum(b.numel() * (2 if b.dtype == torch.int8 and n.endswith("weight_q4") else 1)
+                       for n, b in model.named_buffers()) + sum(p.numel() for p in model.parameters())
+        for _ in range(args.warmup):
+            y = model(*inp)
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(args.steps):
+            y = model(*inp)
+        torch.cuda.synchronize()
+        step_s = (time.perf_counter() - t0) / args.steps
+        finite = bool(torch.isfinite(y).all())
+
+        # block-level parity + CPU baseline inputs: the activations entering block 0
+        img, img_ids, txt, txt_ids, ts, yv, gd = inp
+        dt = torch.bfloat16
+        h_img = fd._linear(model.img_in, img)
+        vec = fd._linear(model.time_in.in_layer, fd.timestep_embedding(ts, cfg.time_dim).to(dt))
+        vec = fd._linear(model.time_in.out_layer, torch.nn.functional.silu(vec))
+        vec = vec + model.guidance_in(fd.timestep_embedding(gd, cfg.time_dim).to(dt)) + model.vector_in(yv)
+        h_txt = fd._linear(model.txt_in, txt)
+        cos, sin = fd.rope_cos_sin(torch.cat([txt_ids, img_ids], 1), cfg.axes_dim, cfg.theta)
+        dblk, sblk = model.double_blocks[0], model.single_blocks[0]
+        g_img, g_txt = dblk(h_img, h_txt, vec, cos, sin)
+        x_cat = torch.cat([g_txt, g_img], 1)
+        g_single = sblk(x_cat, vec, cos, sin)
+        torch.cuda.synchronize()
+
+    def cpu_block(gpu_block, cls):
+        blk = cls(cfg, torch.nn, dtype=torch.float32)
+        sd = {}
+        for name, mod in gpu_block.named_modules():
+            if fd._is_engine_linear(mod):
+                sd[f"{name}.weight"] = dequant_fp32(mod.weight_q4, mod.weight_scale).cpu()
+                sd[f"{name}.bias"] = mod.bias.float().cpu()
+        for name, p in gpu_block.named_parameters():
+            if name.endswith(".scale"):
+                sd[name] = p.float().cpu()
+        blk.load_state_dict(sd)
+        return blk
+
+    threads = torch.get_num_threads()
+    with torch.no_grad():
+        c_cos, c_sin, c_vec = cos.cpu(), sin.cpu(), vec.float().cpu()
+        cd = cpu_block(dblk, fd.DoubleStreamBlock)
+        t0 = time.perf_counter()
+        r_img, r_txt = cd(h_img.float().cpu(), h_txt.float().cpu(), c_vec, c_cos, c_sin)
+        t_double = time.perf_counter() - t0
+        del cd
+        cs = cpu_block(sblk, fd.SingleStreamBlock)
+        t0 = time.perf_counter()
+        r_single = cs(x_cat.float().cpu(), c_vec, c_cos, c_sin)
+        t_single = time.perf_counter() - t0
+        del cs
+
+    def rel(a, b):
+        a, b = a.float().cpu().numpy().astype(np.float64), b.numpy().astype(np.float64)
+        return float(np.abs(a - b).max() / np.abs(b).max())
+
+    e_img, e_txt, e_single = rel(g_img, r_img), rel(g_txt, r_txt), rel(g_single, r_single)
+    gate = 2e-2  # bf16 activations between the block's ops vs an all-fp32 host block
+    lin_flops = cfg.linear_flops(n_side * n_side, n_txt)
+    att_flops = cfg.attention_flops(n_side * n_side, n_txt)
+    cpu_step = cfg.depth_double * t_double + cfg.depth_single * t_single
+    out = {"metric": "DiT step ms (C5, 12B Flux-style, all linears W4A16)", "value": round(step_s * 1e3, 2),
+           "unit": "ms/step", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+           "ms_per_step": round(step_s * 1e3, 2), "higher_is_better": False, "dtype": "bf16 activations, int4 weights",
+           "data": "synthetic (random-init weights quantized on load, seeded N(0,1) inputs)",
+           "config": {"workload": "C5 Flux-style DiT denoise step", "hidden": cfg.hidden, "heads": cfg.heads,
+                      "double_blocks": cfg.depth_double, "single_blocks": cfg.depth_single,
+                      "img_tokens": n_side * n_side, "txt_tokens": n_txt, "batch": 1,
+                      "params": n_params, "attention": "torch SDPA (flash / mem-efficient)"},
+           "linear_tflop_per_step": round(lin_flops / 1e12, 3), "sdpa_tflop_per_step": round(att_flops / 1e12, 3),
+           "effective_tflops": round((lin_flops + att_flops) / step_s / 1e12, 1),
+           "init_s": round(t_init, 1), "output_finite": finite,
+           "parity": {"double_block0_img_rel_err": e_img, "double_block0_txt_rel_err": e_txt,
+                      "single_block0_rel_err": e_single, "gate": gate,
+                      "pass": bool(finite and max(e_img, e_txt, e_single) <= gate)},
+           "cpu_baseline": {"value": round(cpu_step * 1e3, 1), "unit": "ms/step", "cores": threads, "kind": "port",
+                            "sample": f"double block 0 ({t_double:.2f} s) and single block 0 ({t_single:.2f} s) in "
+                                      f"fp32 torch on the host with the dequantized weights, extrapolated x"
+                                      f"{cfg.depth_double} / x{cfg.depth_single} (embedders and final layer "
+                                      f"left out)"}}
+    print(json.dumps(out), flush=True)
 
 
 def dequant_fp32(w_q4, w_scale):
