@@ -52,6 +52,11 @@ SIGNATURES = {
     "qlinear_quantize_int8_per_token": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
     "qlinear_repack_q4_0": (_c_int, [_c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
     "qlinear_w8a8_gemm": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp]),
+    "qlinear_adaln_modulate_f16": (_c_int, [_c_int, _c_vp, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64,
+                                            ctypes.c_float, _c_vp]),
+    "qlinear_qk_norm_rope": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64,
+                                      _c_i64, _c_i64, _c_i64, ctypes.c_float, _c_vp]),
+    "qlinear_gated_residual": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
 }
 
 
@@ -306,3 +311,89 @@ def w8a8_gemm(xq: torch.Tensor, x_scale: torch.Tensor, wq: torch.Tensor, w_scale
                                    _stream_ptr(xq.device))
     _check(rc, "w8a8_gemm")
     return y
+
+
+# ---- fused DiT block glue (csrc/dit_fused.hip) -----------------------------------------------
+def adaln_modulate_f16(x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor,
+                       eps: float = 1e-6) -> tuple[torch.Tensor, torch.Tensor]:
+    """LayerNorm(x) * (1 + scale) + shift for x [M, K] (shift / scale [K], shared by every row),
+    returned as the W4A16 GEMM's fp16 operand: (x16 [M, K] fp16, row_scale [M] fp32), to be
+    passed to w4a16_gemm(x16, ..., row_scale=row_scale)."""
+    lib = load_library()
+    x = _dev_tensor(x, "x")
+    shift = _dev_tensor(shift, "shift").reshape(-1)
+    scale = _dev_tensor(scale, "scale").reshape(-1)
+    if x.dim() != 2 or x.dtype not in _DTYPE_CODE or x.dtype == torch.int32:
+        raise RuntimeError(f"x must be a float [M, K] tensor, got {x.dtype} {tuple(x.shape)}")
+    M, K = x.shape
+    if shift.dtype != scale.dtype or shift.numel() != K or scale.numel() != K or shift.dtype == torch.int32:
+        raise RuntimeError(f"shift and scale must be float [{K}] tensors of one dtype, got {shift.dtype} "
+                           f"{tuple(shift.shape)} / {scale.dtype} {tuple(scale.shape)}")
+    x16 = torch.empty((M, K), dtype=torch.float16, device=x.device)
+    rs = torch.empty((M,), dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        rc = lib.qlinear_adaln_modulate_f16(_DTYPE_CODE[x.dtype], x.data_ptr(), _DTYPE_CODE[shift.dtype],
+                                            shift.data_ptr(), scale.data_ptr(), x16.data_ptr(), rs.data_ptr(), M, K,
+                                            float(eps), _stream_ptr(x.device))
+    _check(rc, "adaln_modulate_f16")
+    return x16, rs
+
+
+def qk_norm_rope(qkv: torch.Tensor, q_norm: torch.Tensor, k_norm: torch.Tensor, cos: torch.Tensor,
+                 sin: torch.Tensor, heads: int, out: tuple | None = None, l_offset: int = 0,
+                 eps: float = 1e-6) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """qkv [L, 3 * heads * 128] -> q, k, v [heads, L_out, 128] with RMSNorm (scales q_norm /
+    k_norm [128]) and RoPE (cos / sin fp32 [L_out, 64]) on q and k, written to rows
+    [l_offset, l_offset + L) of `out` (three [heads, L_out, 128] tensors; new ones with
+    L_out = L when None)."""
+    lib = load_library()
+    qkv = _dev_tensor(qkv, "qkv")
+    if qkv.dtype not in (torch.bfloat16, torch.float16) or qkv.dim() != 2 or qkv.shape[1] != 3 * heads * 128:
+        raise RuntimeError(f"qkv must be a bfloat16/float16 [L, {3 * heads * 128}] tensor, got {qkv.dtype} "
+                           f"{tuple(qkv.shape)}")
+    L = qkv.shape[0]
+    qn = _dev_tensor(q_norm, "q_norm").to(qkv.dtype)
+    kn = _dev_tensor(k_norm, "k_norm").to(qkv.dtype)
+    cos = _dev_tensor(cos, "cos").float().reshape(-1, 64)
+    sin = _dev_tensor(sin, "sin").float().reshape(-1, 64)
+    if out is None:
+        out = tuple(torch.empty((heads, L, 128), dtype=qkv.dtype, device=qkv.device) for _ in range(3))
+    for t in out:
+        if t.dtype != qkv.dtype or t.dim() != 3 or t.shape[0] != heads or t.shape[2] != 128 or not t.is_contiguous():
+            raise RuntimeError(f"outputs must be contiguous {qkv.dtype} [{heads}, L_out, 128] tensors, got {t.dtype} "
+                               f"{tuple(t.shape)}")
+    L_out = out[0].shape[1]
+    if cos.shape[0] != L_out or sin.shape[0] != L_out or qn.numel() != 128 or kn.numel() != 128:
+        raise RuntimeError(f"cos / sin must be [{L_out}, 64] and the norm scales [128]")
+    with torch.cuda.device(qkv.device):
+        rc = lib.qlinear_qk_norm_rope(_DTYPE_CODE[qkv.dtype], qkv.data_ptr(), qn.data_ptr(), kn.data_ptr(),
+                                      cos.data_ptr(), sin.data_ptr(), out[0].data_ptr(), out[1].data_ptr(),
+                                      out[2].data_ptr(), L, heads, 128, L_out, l_offset, float(eps),
+                                      _stream_ptr(qkv.device))
+    _check(rc, "qk_norm_rope")
+    return out
+
+
+def gated_residual(x: torch.Tensor, gate: torch.Tensor, y: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """x + gate * y for x, y [..., K] and gate [K] (one dtype), into `out` (a new tensor when None;
+    `out` may be x itself for the in-place update)."""
+    lib = load_library()
+    x = _dev_tensor(x, "x")
+    K = x.shape[-1]
+    gate = _dev_tensor(gate, "gate").reshape(-1)
+    y = _dev_tensor(y, "y")
+    if x.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        raise RuntimeError(f"dtype {x.dtype} unsupported")
+    if gate.dtype != x.dtype or y.dtype != x.dtype or gate.numel() != K or y.shape != x.shape:
+        raise RuntimeError(f"gate [{K}] and y {tuple(x.shape)} must have x's dtype {x.dtype}, got {gate.dtype} "
+                           f"{tuple(gate.shape)} / {y.dtype} {tuple(y.shape)}")
+    if out is None:
+        out = torch.empty_like(x)
+    elif not (out.is_cuda and out.is_contiguous() and out.data_ptr() % 16 == 0 and out.shape == x.shape
+              and out.dtype == x.dtype):
+        raise RuntimeError("out must be a contiguous, 16-byte aligned GPU tensor of x's shape and dtype")
+    with torch.cuda.device(x.device):
+        rc = lib.qlinear_gated_residual(_DTYPE_CODE[x.dtype], out.data_ptr(), x.data_ptr(), gate.data_ptr(),
+                                        y.data_ptr(), x.numel() // K if K else 0, K, _stream_ptr(x.device))
+    _check(rc, "gated_residual")
+    return out

@@ -432,4 +432,66 @@ int qlinear_w8a8_gemm(int out_dtype, const int8_t* xq, const float* x_scale, con
   return ok();
 }
 
+int qlinear_adaln_modulate_f16(int x_dtype, const void* x, int mod_dtype, const void* shift, const void* scale,
+                               void* x16, float* row_scale, int64_t M, int64_t K, float eps, void* stream) {
+  if (x_dtype != QL_F32 && x_dtype != QL_F16 && x_dtype != QL_BF16)
+    return fail(QL_ERR_DTYPE, "x dtype %s (%d) unsupported, expected float32/float16/bfloat16", dtype_name(x_dtype),
+                x_dtype);
+  if (mod_dtype != QL_F32 && mod_dtype != QL_F16 && mod_dtype != QL_BF16)
+    return fail(QL_ERR_DTYPE, "shift/scale dtype %s (%d) unsupported, expected float32/float16/bfloat16",
+                dtype_name(mod_dtype), mod_dtype);
+  if (M < 0 || M > INT32_MAX || K <= 0 || K % 8 != 0 || K > 16384)
+    return fail(QL_ERR_SHAPE, "x must be [M, K] with K %% 8 == 0 and K <= 16384, got [%lld, %lld]", (long long)M,
+                (long long)K);
+  if (!(eps >= 0.0f)) return fail(QL_ERR_ARG, "eps must be >= 0, got %g", (double)eps);
+  if (M == 0) return ok();
+  if (!x || !shift || !scale || !x16 || !row_scale)
+    return fail(QL_ERR_ARG, "null x / shift / scale / x16 / row_scale pointer");
+  if (!aligned16(x) || !aligned16(shift) || !aligned16(scale) || !aligned16(x16))
+    return fail(QL_ERR_ALIGN, "x, shift, scale and x16 must be 16-byte aligned");
+  const hipError_t e = adaln_to_f16_launch(x_dtype, mod_dtype, x, shift, scale, x16, row_scale, M, K, eps,
+                                           (hipStream_t)stream);
+  if (e != hipSuccess) return fail(QL_ERR_LAUNCH, "adaln_modulate_f16 launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int qlinear_qk_norm_rope(int dtype, const void* qkv, const void* q_norm, const void* k_norm, const float* cos_t,
+                         const float* sin_t, void* q, void* k, void* v, int64_t L, int64_t H, int64_t D,
+                         int64_t L_out, int64_t l_offset, float eps, void* stream) {
+  if (dtype != QL_F16 && dtype != QL_BF16)
+    return fail(QL_ERR_DTYPE, "dtype %s (%d) unsupported, expected float16/bfloat16", dtype_name(dtype), dtype);
+  if (D != 128) return fail(QL_ERR_SHAPE, "head dim must be 128, got %lld", (long long)D);
+  if (L < 0 || H <= 0 || l_offset < 0 || L_out < 0 || l_offset + L > L_out || L_out > (1 << 24) ||
+      H > 4096 || L * H > ((int64_t)1 << 31))
+    return fail(QL_ERR_SHAPE, "expected qkv [L, 3, H, 128] written to rows [l_offset, l_offset + L) of [H, L_out, 128]; "
+                "got L=%lld H=%lld L_out=%lld l_offset=%lld", (long long)L, (long long)H, (long long)L_out,
+                (long long)l_offset);
+  if (!(eps >= 0.0f)) return fail(QL_ERR_ARG, "eps must be >= 0, got %g", (double)eps);
+  if (L == 0) return ok();
+  if (!qkv || !q_norm || !k_norm || !cos_t || !sin_t || !q || !k || !v)
+    return fail(QL_ERR_ARG, "null qkv / q_norm / k_norm / cos / sin / q / k / v pointer");
+  const void* ptrs[] = {qkv, q_norm, k_norm, cos_t, sin_t, q, k, v};
+  for (const void* p : ptrs)
+    if ((uintptr_t)p & 3u) return fail(QL_ERR_ALIGN, "every pointer must be 4-byte aligned (%p)", p);
+  const hipError_t e = qk_norm_rope_launch(dtype, qkv, q_norm, k_norm, cos_t, sin_t, q, k, v, L, H, L_out, l_offset,
+                                           eps, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(QL_ERR_LAUNCH, "qk_norm_rope launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int qlinear_gated_residual(int dtype, void* out, const void* x, const void* gate, const void* y, int64_t M, int64_t K,
+                           void* stream) {
+  if (dtype != QL_F32 && dtype != QL_F16 && dtype != QL_BF16)
+    return fail(QL_ERR_DTYPE, "dtype %s (%d) unsupported, expected float32/float16/bfloat16", dtype_name(dtype), dtype);
+  if (M < 0 || K <= 0 || K % 8 != 0 || K > INT32_MAX || M > INT64_MAX / 8 / K)
+    return fail(QL_ERR_SHAPE, "x must be [M, K] with K %% 8 == 0, got [%lld, %lld]", (long long)M, (long long)K);
+  if (M == 0) return ok();
+  if (!out || !x || !gate || !y) return fail(QL_ERR_ARG, "null out / x / gate / y pointer");
+  if (!aligned16(out) || !aligned16(x) || !aligned16(gate) || !aligned16(y))
+    return fail(QL_ERR_ALIGN, "out, x, gate and y must be 16-byte aligned");
+  const hipError_t e = gated_residual_launch(dtype, out, x, gate, y, M, K, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(QL_ERR_LAUNCH, "gated_residual launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
 }  // extern "C"

@@ -84,4 +84,14 @@ hipError_t repack_q4_0_launch(const void* raw, void* packed, float* scale, int64
 hipError_t quantize_int8_per_token_launch(int dtype, const void* x, int8_t* q, float* scale,
                                           int64_t M, int64_t K, hipStream_t stream);
 
+// Fused DiT block glue (dit_fused.hip). K % 8 == 0 and K <= 16384 for the LayerNorm kernel;
+// head dim 128 for the q/k kernel; K % 8 == 0 for the residual.
+hipError_t adaln_to_f16_launch(int x_dtype, int mod_dtype, const void* x, const void* shift, const void* scale,
+                               void* x16, float* row_scale, int64_t M, int64_t K, float eps, hipStream_t stream);
+hipError_t qk_norm_rope_launch(int dtype, const void* qkv, const void* q_norm, const void* k_norm, const float* cosv,
+                               const float* sinv, void* q, void* k, void* v, int64_t L, int64_t H, int64_t L_out,
+                               int64_t l0, float eps, hipStream_t stream);
+hipError_t gated_residual_launch(int dtype, void* out, const void* x, const void* gate, const void* y, int64_t M,
+                                 int64_t K, hipStream_t stream);
+
 }  // namespace qlinear

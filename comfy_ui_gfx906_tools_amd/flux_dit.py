@@ -18,6 +18,7 @@ from __future__ import annotations
 
 import math
 from dataclasses import dataclass
+from typing import NamedTuple
 
 import torch
 import torch.nn.functional as F
@@ -76,15 +77,30 @@ def _is_engine_linear(layer) -> bool:
     return isinstance(layer, Gfx906Int4Ops.Linear) and layer.quantized
 
 
-def _linear(layer, x: torch.Tensor, gelu: bool = False, rows: slice | None = None) -> torch.Tensor:
+class Staged(NamedTuple):
+    """A GEMM operand already in the W4A16 kernel's fp16 form: x16 [rows, K] fp16 with per-row
+    power-of-two factors row_scale [rows]; `lead` are the leading dims of the logical tensor and
+    `dtype` its activation dtype (the GEMM's output dtype)."""
+    x16: torch.Tensor
+    row_scale: torch.Tensor
+    lead: tuple
+    dtype: torch.dtype
+
+
+def _linear(layer, x, gelu: bool = False, rows: slice | None = None) -> torch.Tensor:
     """layer(x), optionally followed by GELU-tanh, optionally restricted to output rows `rows`
-    of the weight. Engine layers fuse the GELU into the GEMM epilogue and take row slices of
-    weight_q4 / weight_scale / bias as views (rows of the packed layout are contiguous)."""
+    of the weight. Engine layers fuse the GELU into the GEMM epilogue, take row slices of
+    weight_q4 / weight_scale / bias as views (rows of the packed layout are contiguous) and
+    accept a Staged operand."""
     if _is_engine_linear(layer):
         wq, ws, b = layer.weight_q4, layer.weight_scale, layer.bias
         if rows is not None:
             wq, ws = wq[rows], ws[rows]
             b = b[rows] if b is not None else None
+        if isinstance(x, Staged):
+            y = _lib.w4a16_gemm(x.x16, wq, ws, b.to(x.dtype) if b is not None else None, out_dtype=x.dtype,
+                                row_scale=x.row_scale, gelu=gelu)
+            return y.reshape(*x.lead, wq.shape[0])
         shape = x.shape
         y = _lib.w4a16_gemm(x.reshape(-1, shape[-1]), wq, ws, b.to(x.dtype) if b is not None else None,
                             out_dtype=x.dtype, gelu=gelu)
@@ -167,6 +183,41 @@ def _modulate(x, shift, scale):
     return _layer_norm(x) * (1 + scale) + shift
 
 
+# ---- the engine path's fused glue (csrc/dit_fused.hip); batch items one call each -----------
+def _adaln(x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor) -> Staged:
+    """_modulate(x, shift, scale) for x [B, L, K], shift / scale [B, 1, K], as the fp16 GEMM operand."""
+    B, L, K = x.shape
+    parts = [_lib.adaln_modulate_f16(x[b], shift[b].reshape(-1), scale[b].reshape(-1)) for b in range(B)]
+    if B == 1:
+        x16, rs = parts[0]
+    else:
+        x16, rs = torch.cat([p[0] for p in parts]), torch.cat([p[1] for p in parts])
+    return Staged(x16, rs, (B, L), x.dtype)
+
+
+def _residual(x: torch.Tensor, gate: torch.Tensor, y: torch.Tensor, inplace: bool = False) -> torch.Tensor:
+    """x + gate * y for x, y [B, L, K] and gate [B, 1, K]; into x itself when inplace."""
+    out = x if inplace else torch.empty_like(x)
+    for b in range(x.shape[0]):
+        _lib.gated_residual(x[b], gate[b].reshape(-1), y[b], out=out[b])
+    return out
+
+
+def _heads_into(attn: "SelfAttention", qkv: torch.Tensor, cos, sin, q, k, v, l_offset: int) -> None:
+    """QK-norm + RoPE of qkv [B, Lx, 3 H D] into rows [l_offset, l_offset + Lx) of q, k, v [B, H, L, D]."""
+    for b in range(qkv.shape[0]):
+        _lib.qk_norm_rope(qkv[b], attn.norm.query_norm.scale, attn.norm.key_norm.scale, cos[b, 0], sin[b, 0],
+                          attn.heads, out=(q[b], k[b], v[b]), l_offset=l_offset)
+
+
+def _sdpa(q, k, v) -> torch.Tensor:
+    """SDPA on [B, H, L, D] (flash / memory-efficient kernels only) -> [B, L, H D]."""
+    from torch.nn.attention import SDPBackend, sdpa_kernel
+    with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
+        o = F.scaled_dot_product_attention(q, k, v)
+    return o.transpose(1, 2).flatten(2)
+
+
 class MLPEmbedder(torch.nn.Module):
     def __init__(self, in_dim, hidden, ops, device=None, dtype=None):
         super().__init__()
@@ -219,6 +270,8 @@ class DoubleStreamBlock(torch.nn.Module):
                                                           ops.Linear(m, h, bias=True, device=device, dtype=dtype)))
 
     def forward(self, img, txt, vec, cos, sin):
+        if _is_engine_linear(self.img_attn.qkv) and img.is_cuda:
+            return self._forward_engine(img, txt, vec, cos, sin)
         i_sh1, i_sc1, i_g1, i_sh2, i_sc2, i_g2 = self.img_mod(vec)
         t_sh1, t_sc1, t_g1, t_sh2, t_sc2, t_g2 = self.txt_mod(vec)
         qs, ks, vs = [], [], []
@@ -235,6 +288,26 @@ class DoubleStreamBlock(torch.nn.Module):
         txt = txt + t_g2 * _linear(self.txt_mlp[2], _linear(self.txt_mlp[0], _modulate(txt, t_sh2, t_sc2), gelu=True))
         return img, txt
 
+    def _forward_engine(self, img, txt, vec, cos, sin):
+        """forward() with the fused kernels: adaLN straight into the GEMM operand, QK-norm + RoPE
+        written into the joint [txt | img] q / k / v, gated residuals in one pass each."""
+        i_sh1, i_sc1, i_g1, i_sh2, i_sc2, i_g2 = self.img_mod(vec)
+        t_sh1, t_sc1, t_g1, t_sh2, t_sc2, t_g2 = self.txt_mod(vec)
+        B, n_img, _ = img.shape
+        n_txt = txt.shape[1]
+        D = self.img_attn.qkv.in_features // self.heads
+        q, k, v = (torch.empty(B, self.heads, n_txt + n_img, D, dtype=img.dtype, device=img.device) for _ in range(3))
+        _heads_into(self.txt_attn, _linear(self.txt_attn.qkv, _adaln(txt, t_sh1, t_sc1)), cos, sin, q, k, v, 0)
+        _heads_into(self.img_attn, _linear(self.img_attn.qkv, _adaln(img, i_sh1, i_sc1)), cos, sin, q, k, v, n_txt)
+        o = _sdpa(q, k, v)
+        img = _residual(img, i_g1, _linear(self.img_attn.proj, o[:, n_txt:]))
+        h = _linear(self.img_mlp[0], _adaln(img, i_sh2, i_sc2), gelu=True)
+        img = _residual(img, i_g2, _linear(self.img_mlp[2], h), inplace=True)
+        txt = _residual(txt, t_g1, _linear(self.txt_attn.proj, o[:, :n_txt]))
+        h = _linear(self.txt_mlp[0], _adaln(txt, t_sh2, t_sc2), gelu=True)
+        txt = _residual(txt, t_g2, _linear(self.txt_mlp[2], h), inplace=True)
+        return img, txt
+
 
 class SingleStreamBlock(torch.nn.Module):
     def __init__(self, cfg: FluxDiTConfig, ops, device=None, dtype=None):
@@ -247,6 +320,8 @@ class SingleStreamBlock(torch.nn.Module):
         self.modulation = Modulation(h, False, ops, device, dtype)
 
     def forward(self, x, vec, cos, sin):
+        if _is_engine_linear(self.linear1) and x.is_cuda:
+            return self._forward_engine(x, vec, cos, sin)
         shift, scale, gate = self.modulation(vec)
         xm = _modulate(x, shift, scale)
         h3 = 3 * self.hidden
@@ -257,6 +332,24 @@ class SingleStreamBlock(torch.nn.Module):
         q, k = self.norm(q, k)
         o = attention(q, k, v, cos, sin)
         return x + gate * _linear(self.linear2, torch.cat([o, mlp], dim=-1))
+
+    def _forward_engine(self, x, vec, cos, sin):
+        shift, scale, gate = self.modulation(vec)
+        st = _adaln(x, shift, scale)
+        h3 = 3 * self.hidden
+        B, L, _ = x.shape
+        D = self.hidden // self.heads
+        # linear2's input [attention | gelu(mlp)] assembled in one buffer
+        cat = torch.empty(B, L, self.linear2.in_features, dtype=x.dtype, device=x.device)
+        q, k, v = (torch.empty(B, self.heads, L, D, dtype=x.dtype, device=x.device) for _ in range(3))
+        for b in range(B):
+            _lib.qk_norm_rope(_linear(self.linear1, Staged(st.x16[b * L:(b + 1) * L], st.row_scale[b * L:(b + 1) * L],
+                                                           (L,), x.dtype), rows=slice(0, h3)),
+                              self.norm.query_norm.scale, self.norm.key_norm.scale, cos[b, 0], sin[b, 0], self.heads,
+                              out=(q[b], k[b], v[b]))
+        cat[..., h3 // 3:] = _linear(self.linear1, st, gelu=True, rows=slice(h3, None))
+        cat[..., :h3 // 3] = _sdpa(q, k, v)
+        return _residual(x, gate, _linear(self.linear2, cat))
 
 
 class LastLayer(torch.nn.Module):
@@ -269,6 +362,8 @@ class LastLayer(torch.nn.Module):
 
     def forward(self, x, vec):
         shift, scale = _linear(self.adaLN_modulation[1], F.silu(vec)).chunk(2, dim=-1)
+        if _is_engine_linear(self.linear) and x.is_cuda:
+            return _linear(self.linear, _adaln(x.contiguous(), shift[:, None], scale[:, None]))
         return _linear(self.linear, _modulate(x, shift[:, None], scale[:, None]))
 
 

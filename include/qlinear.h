@@ -151,6 +151,39 @@ int qlinear_w8a8_gemm(int out_dtype, const int8_t* xq, const float* x_scale, con
                       const float* w_scale, const void* bias, void* y, int64_t M, int64_t N,
                       int64_t K, void* stream);
 
+/* ---------------------------------------------------------------------------------------
+ * Fused DiT block glue. No counterpart in the reference: its node patches only the Linears of
+ * ComfyUI's Flux model (nodes/ComfyUI-Gfx906Int4/nodes.py:71-124, 447-599) and the layer norms,
+ * modulation, QK-norm, RoPE and gated residuals run as separate torch ops around them. Each entry
+ * point is one HBM pass, computes in fp32 and rounds once.
+ * ------------------------------------------------------------------------------------- */
+/* adaLN: y = LayerNorm(x[m, :]) (no affine, biased variance, eps) * (1 + scale) + shift, with
+ * shift / scale [K] shared by all rows (one batch item), written as the fp16 operand of
+ * qlinear_w4a16_gemm: x16 = y * 2^-e_m rounded to fp16, e_m such that max|y[m, :]| * 2^-e_m is in
+ * [2^14, 2^15) (after the rounding, max|x16[m, :]| <= 2^15), row_scale[m] = 2^e_m
+ * (pass both to qlinear_w4a16_gemm with x_dtype QL_F16). x fp32/fp16/bf16, shift/scale of
+ * mod_dtype; K % 8 == 0, K <= 16384; x, shift, scale, x16 16-byte aligned. */
+int qlinear_adaln_modulate_f16(int x_dtype, const void* x, int mod_dtype, const void* shift,
+                               const void* scale, void* x16, float* row_scale, int64_t M,
+                               int64_t K, float eps, void* stream);
+
+/* QK-norm + RoPE + head split of a qkv projection [L, 3, H, D] (q, k, v blocks of H heads):
+ * q[h, l_offset + l, :] = rope(rmsnorm(q_in[l, h, :]) * q_norm), likewise k with k_norm,
+ * v[h, l_offset + l, :] = v_in[l, h, :]; q, k, v are [H, L_out, D] (the attention layout), so
+ * two calls with offsets 0 and L_txt assemble a joint text + image sequence. rmsnorm = x *
+ * rsqrt(mean(x^2) + eps); rope rotates pairs (2j, 2j + 1) by cos/sin[l_offset + l, j] (fp32
+ * [L_out, D/2]). dtype fp16/bf16 for qkv, norms and outputs; D == 128; 4-byte alignment. */
+int qlinear_qk_norm_rope(int dtype, const void* qkv, const void* q_norm, const void* k_norm,
+                         const float* cos_t, const float* sin_t, void* q, void* k, void* v,
+                         int64_t L, int64_t H, int64_t D, int64_t L_out, int64_t l_offset,
+                         float eps, void* stream);
+
+/* Gated residual: out[m, k] = x[m, k] + gate[k] * y[m, k]; out may be x (in place) but must
+ * not overlap it otherwise; out, x, gate, y of one dtype (fp32/fp16/bf16), K % 8 == 0, 16-byte
+ * aligned. */
+int qlinear_gated_residual(int dtype, void* out, const void* x, const void* gate, const void* y,
+                           int64_t M, int64_t K, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

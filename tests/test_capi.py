@@ -139,6 +139,36 @@ def test_quantizer_and_w8a8_argument_checks(lib):
     assert lib.qlinear_rows_to_f16(3, None, None, None, 4, 16, None) == QL_ERR_DTYPE
 
 
+def test_fused_dit_entry_points_check_arguments(lib):
+    """The fused DiT glue entry points reject bad arguments before any launch."""
+    p16 = ctypes.c_void_p(256)
+    adaln = lib.qlinear_adaln_modulate_f16
+    assert adaln(3, None, 2, None, None, None, None, 4, 64, 1e-6, None) == QL_ERR_DTYPE
+    assert adaln(2, None, 3, None, None, None, None, 4, 64, 1e-6, None) == QL_ERR_DTYPE
+    assert adaln(2, None, 2, None, None, None, None, 4, 60, 1e-6, None) == QL_ERR_SHAPE
+    assert adaln(2, None, 2, None, None, None, None, 4, 16392, 1e-6, None) == QL_ERR_SHAPE
+    assert "K <= 16384" in _err(lib)
+    assert adaln(2, None, 2, None, None, None, None, 4, 64, -1.0, None) == QL_ERR_ARG
+    assert adaln(2, None, 2, None, None, None, None, 0, 64, 1e-6, None) == QL_OK
+    assert adaln(2, None, 2, None, None, None, None, 4, 64, 1e-6, None) == QL_ERR_ARG
+    assert adaln(2, ctypes.c_void_p(258), 2, p16, p16, p16, p16, 4, 64, 1e-6, None) == QL_ERR_ALIGN
+    qk = lib.qlinear_qk_norm_rope
+    assert qk(0, None, None, None, None, None, None, None, None, 4, 2, 128, 4, 0, 1e-6, None) == QL_ERR_DTYPE
+    assert qk(2, None, None, None, None, None, None, None, None, 4, 2, 64, 4, 0, 1e-6, None) == QL_ERR_SHAPE
+    assert qk(2, None, None, None, None, None, None, None, None, 4, 2, 128, 6, 3, 1e-6, None) == QL_ERR_SHAPE
+    assert "l_offset" in _err(lib)
+    assert qk(2, None, None, None, None, None, None, None, None, 0, 2, 128, 6, 3, 1e-6, None) == QL_OK
+    assert qk(2, None, None, None, None, None, None, None, None, 4, 2, 128, 6, 2, 1e-6, None) == QL_ERR_ARG
+    assert qk(2, p16, p16, p16, p16, p16, p16, p16, ctypes.c_void_p(258), 4, 2, 128, 6, 2, 1e-6,
+              None) == QL_ERR_ALIGN
+    res = lib.qlinear_gated_residual
+    assert res(3, None, None, None, None, 4, 64, None) == QL_ERR_DTYPE
+    assert res(2, None, None, None, None, 4, 12, None) == QL_ERR_SHAPE
+    assert res(2, None, None, None, None, 0, 64, None) == QL_OK
+    assert res(2, None, None, None, None, 4, 64, None) == QL_ERR_ARG
+    assert res(2, p16, ctypes.c_void_p(264), p16, p16, 4, 64, None) == QL_ERR_ALIGN
+
+
 def test_error_text_is_per_thread(lib):
     import threading
     assert lib.qlinear_quantize_int4(3, 0, None, None, None, 4, 64, None) == QL_ERR_DTYPE
