@@ -102,17 +102,15 @@ int64_t tile256_whole(int64_t tiles, int cus) {
   return (rem > 0 && 2 * rem <= cus) ? tiles - rem : tiles;
 }
 
-// Makespan model in units of one 256 x 256 tile's time on a CU: the 256 x 256 kernel runs its full
-// rounds plus a half-tile round (about 0.6 of a round) or one more whole round; the 128-row kernel
-// balances its tiles over all CUs (K-cut last wave) but spends about 1.3x the time per flop
-// (measured at the BASELINE shapes).
+// 256 x 256 tiles once there are at least a quarter as many as CUs. Measured on MI355X (bf16 x via
+// the fp16 staging, Flux DiT shapes): the 128-row kernel spends 1.6-2.2x the time per flop, so the
+// 256 x 256 kernel wins even with most CUs idle (M=4096 N=3072 K=3072, 192 tiles: 80 vs 128 us;
+// M=512 N=9216 K=3072, 72 tiles: 46 vs 103 us); with fewer tiles the 128-row kernel's K cuts spread
+// the work over the CUs and win (M=512 N=3072, 24 tiles: K=3072 33 vs 40 us, K=12288 63 vs 139 us).
 bool prefer_tile256(int64_t M, int64_t N, int64_t K, int cus) {
   if (K % 64 != 0) return false;
   const int64_t tiles = ((M + 255) / 256) * ((N + 255) / 256);
-  const int64_t whole = tile256_whole(tiles, cus);
-  const double t256 = (double)(whole / cus) + (whole < tiles ? 0.6 : (whole % cus ? 1.0 : 0.0));
-  const double t128 = 1.3 * (double)tiles / cus;
-  return t256 <= t128;
+  return 4 * tiles >= cus;
 }
 
 // Up to 4 rows of 16-bit activations go to the VALU kernel (configuration 7), read as they are.
