@@ -101,7 +101,12 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W
   int tm, tn;
   tile_coords(p.tile_base + g / kSub, p.tiles_m, p.tiles_n, kT256GroupM, tm, tn);
   const int m0 = tm * 256 + (g % kSub) * BM, n0 = tn * BN;
-  const int rows = min(M - m0, BM), cols = min(N - n0, BN);
+  // The second 128-row half of the last tile row lies wholly past M when M % 256 is in (0, 128]:
+  // nothing to compute or store. The exit is uniform over the workgroup and precedes every barrier
+  // and DMA. (Without it `rows` would be negative and the activation descriptor's range would wrap
+  // to ~4 GB past the end of x.)
+  if (m0 >= M) return;
+  const int rows = max(0, min(M - m0, BM)), cols = max(0, min(N - n0, BN));
 
   const rsrc_t rs_a = make_rsrc((const uint16_t*)p.x + (size_t)m0 * K, (uint32_t)rows * K * 2);
   const rsrc_t rs_b = make_rsrc((const uint8_t*)p.wq + (size_t)n0 * (K / 2), (uint32_t)cols * (K / 2));

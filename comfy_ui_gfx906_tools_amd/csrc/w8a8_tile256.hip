@@ -73,7 +73,8 @@ __global__ __launch_bounds__(64 * kQ8Waves) void w8a8_tile256_kernel(W8A8Params 
   int tm, tn;
   tile_coords(g, p.tiles_m, p.tiles_n, kQ8GroupM, tm, tn);
   const int m0 = tm * kQ8BM, n0 = tn * kQ8BN;
-  const int rows = min(M - m0, kQ8BM), cols = min(N - n0, kQ8BN);
+  // clamped at 0 so a descriptor range can never wrap (tiles start inside M and N here)
+  const int rows = max(0, min(M - m0, kQ8BM)), cols = max(0, min(N - n0, kQ8BN));
   const rsrc_t rs_a = make_rsrc(p.xq + (size_t)m0 * K, (uint32_t)rows * K);
   const rsrc_t rs_b = make_rsrc(p.wq + (size_t)n0 * K, (uint32_t)cols * K);
   const rsrc_t rs_none = make_rsrc(p.xq, 0);

@@ -170,10 +170,12 @@ def _run_cfg(x, wq, ws, bias=None, out_dtype=torch.float32, cfg=None, bf16_mfma=
 
 @pytest.mark.parametrize("cfg", ALL_CFGS)
 @pytest.mark.parametrize("M,N,K,xdt", [(300, 200, 192, torch.bfloat16), (513, 777, 640, torch.float16),
-                                       (256, 512, 3072, torch.bfloat16)])
+                                       (256, 512, 3072, torch.bfloat16), (257, 300, 1024, torch.float16)])
 def test_w4a16_every_config_vs_oracle(cfg, M, N, K, xdt):
     """Ragged M and N (tiles past the edges), bias, fp32 out: each configuration within the gate,
-    and two runs bit-identical."""
+    and two runs bit-identical. M = 513 and 257 leave one row in the last 256-row tile, so on the
+    256 x 256 kernel the second 128-row half of that tile lies wholly past M (regression: its
+    activation descriptor once took a wrapped range past the end of x and faulted the GPU)."""
     print(f"case cfg={cfg} M={M} N={N} K={K} x={xdt}", flush=True)
     x, wq, ws = seeded_linear(M, N, K, seed=M + 3 * N + K + cfg, x_dtype=xdt)
     bias = torch.randn(N, generator=torch.Generator().manual_seed(cfg))
