@@ -24,7 +24,7 @@ import torch
 import torch.nn.functional as F
 
 from . import _lib
-from .ops import Gfx906Int4Ops, quantize_pack_int4
+from .ops import Gfx906Int4Ops, apply_group_rotation, get_group_rotation, quantize_pack_int4
 
 
 @dataclass(frozen=True)
@@ -77,6 +77,11 @@ def _is_engine_linear(layer) -> bool:
     return isinstance(layer, Gfx906Int4Ops.Linear) and layer.quantized
 
 
+def _fusable(layer) -> bool:
+    """Engine layer without activation rotation: it can take the fused adaLN operand."""
+    return _is_engine_linear(layer) and not layer.rotation_group
+
+
 class Staged(NamedTuple):
     """A GEMM operand already in the W4A16 kernel's fp16 form: x16 [rows, K] fp16 with per-row
     power-of-two factors row_scale [rows]; `lead` are the leading dims of the logical tensor and
@@ -98,12 +103,17 @@ def _linear(layer, x, gelu: bool = False, rows: slice | None = None) -> torch.Te
             wq, ws = wq[rows], ws[rows]
             b = b[rows] if b is not None else None
         if isinstance(x, Staged):
+            if layer.rotation_group:
+                raise RuntimeError("a layer with activation rotation takes a plain activation tensor")
             y = _lib.w4a16_gemm(x.x16, wq, ws, b.to(x.dtype) if b is not None else None, out_dtype=x.dtype,
                                 row_scale=x.row_scale, gelu=gelu)
             return y.reshape(*x.lead, wq.shape[0])
         shape = x.shape
-        y = _lib.w4a16_gemm(x.reshape(-1, shape[-1]), wq, ws, b.to(x.dtype) if b is not None else None,
-                            out_dtype=x.dtype, gelu=gelu)
+        x2 = x.reshape(-1, shape[-1])
+        if layer.rotation_group:  # the weight was folded through the rotation (as int4_linear does)
+            g = layer.rotation_group
+            x2 = apply_group_rotation(x2.float(), get_group_rotation(shape[-1], g, x2.device), g)
+        y = _lib.w4a16_gemm(x2, wq, ws, b.to(x.dtype) if b is not None else None, out_dtype=x.dtype, gelu=gelu)
         return y.reshape(*shape[:-1], wq.shape[0])
     w, b = layer.weight, layer.bias
     if rows is not None:
@@ -270,7 +280,7 @@ class DoubleStreamBlock(torch.nn.Module):
                                                           ops.Linear(m, h, bias=True, device=device, dtype=dtype)))
 
     def forward(self, img, txt, vec, cos, sin):
-        if _is_engine_linear(self.img_attn.qkv) and img.is_cuda:
+        if img.is_cuda and all(_fusable(m) for m in self.modules() if isinstance(m, Gfx906Int4Ops.Linear)):
             return self._forward_engine(img, txt, vec, cos, sin)
         i_sh1, i_sc1, i_g1, i_sh2, i_sc2, i_g2 = self.img_mod(vec)
         t_sh1, t_sc1, t_g1, t_sh2, t_sc2, t_g2 = self.txt_mod(vec)
@@ -320,7 +330,7 @@ class SingleStreamBlock(torch.nn.Module):
         self.modulation = Modulation(h, False, ops, device, dtype)
 
     def forward(self, x, vec, cos, sin):
-        if _is_engine_linear(self.linear1) and x.is_cuda:
+        if x.is_cuda and all(_fusable(m) for m in self.modules() if isinstance(m, Gfx906Int4Ops.Linear)):
             return self._forward_engine(x, vec, cos, sin)
         shift, scale, gate = self.modulation(vec)
         xm = _modulate(x, shift, scale)
@@ -362,7 +372,7 @@ class LastLayer(torch.nn.Module):
 
     def forward(self, x, vec):
         shift, scale = _linear(self.adaLN_modulation[1], F.silu(vec)).chunk(2, dim=-1)
-        if _is_engine_linear(self.linear) and x.is_cuda:
+        if _fusable(self.linear) and x.is_cuda:
             return _linear(self.linear, _adaln(x.contiguous(), shift[:, None], scale[:, None]))
         return _linear(self.linear, _modulate(x, shift[:, None], scale[:, None]))
 

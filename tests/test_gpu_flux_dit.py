@@ -8,6 +8,7 @@ import pytest
 import torch
 
 from comfy_ui_gfx906_tools_amd import flux_dit as fd
+from tests.conftest import golden_path
 from tests.gpu_util import dequant_torch, rel_max_err
 
 pytestmark = pytest.mark.gpu
@@ -66,3 +67,43 @@ def test_single_block_split_linear1_matches_whole():
     ref = torch.nn.functional.gelu(whole[:, h3:].float(), approximate="tanh")
     err = (mlp.float() - ref).abs().max().item()
     assert err <= 2.0 ** -7 * max(1.0, ref.abs().max().item()), err
+
+
+@pytest.mark.parametrize("rotate", [False, True])
+def test_transcoded_float_dit_matches_twin(rotate):
+    """A float DiT on the GPU, transcoded in place by the Transcode node's code (HIP quantizer,
+    optional Hadamard rotation folded into the weights), against the fp32 host twin whose weights
+    are the dequantized codes -- times the group rotation R when rotated, since
+    rotate(x) @ Wq^T = x @ (Wq R)^T per group."""
+    from comfy_ui_gfx906_tools_amd import nodes
+    from oracle import qlinear_oracle as orc
+    cfg = fd.FluxDiTConfig.tiny()
+    print(f"transcoded tiny DiT rotate={rotate}", flush=True)
+    with torch.no_grad():
+        m = fd.FluxDiT(cfg, ops=torch.nn, device="cuda", dtype=torch.bfloat16)
+        fd.init_random_(m, seed=13)
+        converted, skipped, _ = nodes.transcode_linears(m, rotate=rotate)
+        assert skipped == 0 and converted == sum(1 for x in m.modules() if isinstance(x, fd.Gfx906Int4Ops.Linear))
+        inp = fd.synthetic_inputs(cfg, 8, 16, seed=1, device="cuda")
+        y = m(*inp)
+        torch.cuda.synchronize()
+        ref_model = fd.FluxDiT(cfg, ops=torch.nn, dtype=torch.float32)
+        sd = {}
+        signs = np.load(golden_path("rotation_signs.npz"))
+        for name, mod in m.named_modules():
+            if fd._is_engine_linear(mod):
+                w = dequant_torch(mod.weight_q4, mod.weight_scale).cpu().double().numpy()
+                g = mod.rotation_group
+                assert bool(g) == rotate
+                if g:
+                    R = orc.group_rotation(signs[f"signs_{g}"]).astype(np.float64)
+                    w = (w.reshape(w.shape[0], -1, g) @ R).reshape(w.shape)
+                sd[f"{name}.weight"] = torch.from_numpy(w).float()
+                sd[f"{name}.bias"] = mod.bias.float().cpu()
+        for name, p in m.named_parameters():
+            if name.endswith(".scale"):
+                sd[name] = p.float().cpu()
+        ref_model.load_state_dict(sd)
+        ref = ref_model(*[t.float().cpu() for t in inp])
+    err = rel_max_err(y.float().cpu().numpy(), ref.numpy())
+    assert np.isfinite(err) and err <= GATE, f"max rel err {err:.3e}"
