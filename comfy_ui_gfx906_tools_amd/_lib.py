@@ -56,6 +56,8 @@ SIGNATURES = {
                                             ctypes.c_float, _c_vp]),
     "qlinear_qk_norm_rope": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64,
                                       _c_i64, _c_i64, _c_i64, ctypes.c_float, _c_vp]),
+    "qlinear_w4a4_gemm": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int,
+                                   _c_vp]),
     "qlinear_gated_residual": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
 }
 
@@ -310,6 +312,48 @@ def w8a8_gemm(xq: torch.Tensor, x_scale: torch.Tensor, wq: torch.Tensor, w_scale
                                    bias.data_ptr() if bias is not None else None, y.data_ptr(), M, N, K,
                                    _stream_ptr(xq.device))
     _check(rc, "w8a8_gemm")
+    return y
+
+
+def w4a4_gemm(a_q4: torch.Tensor, a_scale: torch.Tensor, b_q4: torch.Tensor, b_scale: torch.Tensor,
+              bias: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float32,
+              qblock: int = 32) -> torch.Tensor:
+    """y[M, N] from block-scaled int4 activations (quantize_int4) and int4 weights with the
+    reference's per-block fmaf accumulation in K order (see include/qlinear.h)."""
+    lib = load_library()
+    a_q4, b_q4 = _dev_tensor(a_q4, "A_packed"), _dev_tensor(b_q4, "B_packed")
+    if a_q4.device != b_q4.device:
+        raise RuntimeError(f"A and B must be on the same device, got {a_q4.device} / {b_q4.device}")
+    if a_q4.dtype != torch.int8 or b_q4.dtype != torch.int8:
+        raise RuntimeError(f"packed tensors must be int8, got {a_q4.dtype} / {b_q4.dtype}")
+    if a_q4.dim() != 2 or b_q4.dim() != 2 or a_q4.shape[1] != b_q4.shape[1] or a_q4.shape[1] % 16 != 0:
+        raise RuntimeError(f"expected A [M, K/2], B [N, K/2], K % 32 == 0; got A {tuple(a_q4.shape)} B "
+                           f"{tuple(b_q4.shape)}")
+    if qblock not in (32, 16):
+        raise RuntimeError(f"qblock must be 32 or 16, got {qblock}")
+    a_scale, b_scale = _dev_tensor(a_scale, "A_scale"), _dev_tensor(b_scale, "B_scale")
+    if a_scale.dtype != torch.float32 or b_scale.dtype != torch.float32:
+        raise RuntimeError("scales must be float32")
+    M, N, K = a_q4.shape[0], b_q4.shape[0], a_q4.shape[1] * 2
+    if a_scale.numel() != M * K // qblock or b_scale.numel() != N * K // qblock:
+        raise RuntimeError(f"scales must be [M, K/{qblock}] / [N, K/{qblock}] = {M * K // qblock} / {N * K // qblock} "
+                           f"elements, got {a_scale.numel()} / {b_scale.numel()}")
+    if out_dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        raise RuntimeError(f"unsupported dtype {out_dtype}, expected float32/float16/bfloat16")
+    if bias is not None:
+        bias = _dev_tensor(bias, "bias")
+        if bias.dtype != out_dtype:
+            raise RuntimeError(f"bias dtype {bias.dtype} != out dtype {out_dtype}")
+        if bias.numel() != N:
+            raise RuntimeError(f"bias must have {N} elements, got {bias.numel()}")
+    y = torch.empty((M, N), dtype=out_dtype, device=a_q4.device)
+    if M == 0:
+        return y
+    with torch.cuda.device(a_q4.device):
+        rc = lib.qlinear_w4a4_gemm(_DTYPE_CODE[out_dtype], a_q4.data_ptr(), a_scale.data_ptr(), b_q4.data_ptr(),
+                                   b_scale.data_ptr(), bias.data_ptr() if bias is not None else None, y.data_ptr(),
+                                   M, N, K, qblock, _stream_ptr(a_q4.device))
+    _check(rc, "w4a4_gemm")
     return y
 
 

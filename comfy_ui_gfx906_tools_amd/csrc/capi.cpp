@@ -492,4 +492,38 @@ int qlinear_gated_residual(int dtype, void* out, const void* x, const void* gate
   return ok();
 }
 
+int qlinear_w4a4_gemm(int out_dtype, const void* a_q4, const float* a_scale, const void* b_q4, const float* b_scale,
+                      const void* bias, void* y, int64_t M, int64_t N, int64_t K, int qblock, void* stream) {
+  if (out_dtype != QL_F32 && out_dtype != QL_F16 && out_dtype != QL_BF16)
+    return fail(QL_ERR_DTYPE, "out dtype %s (%d) unsupported, expected float32/float16/bfloat16", dtype_name(out_dtype),
+                out_dtype);
+  if (qblock != 32 && qblock != 16) return fail(QL_ERR_ARG, "qblock must be 32 or 16, got %d", qblock);
+  if (M < 0 || N <= 0 || K < 32 || K % 32 != 0 || M > INT32_MAX / 2 || N > INT32_MAX / 2 || K > (1 << 30))
+    return fail(QL_ERR_SHAPE, "expected A [M, K/2], B [N, K/2] with K %% 32 == 0, K >= 32, N > 0; got M=%lld N=%lld "
+                "K=%lld", (long long)M, (long long)N, (long long)K);
+  const int64_t tiles = ((M + 127) / 128) * ((N + 127) / 128);
+  if (tiles > INT32_MAX) return fail(QL_ERR_SHAPE, "too many 128 x 128 tiles (M=%lld N=%lld)", (long long)M, (long long)N);
+  if (M == 0) return ok();
+  if (!a_q4 || !a_scale || !b_q4 || !b_scale || !y) return fail(QL_ERR_ARG, "null a_q4 / a_scale / b_q4 / b_scale / y pointer");
+  if (!aligned16(a_q4) || !aligned16(b_q4)) return fail(QL_ERR_ALIGN, "a_q4 and b_q4 must be 16-byte aligned");
+  if (((uintptr_t)a_scale & 3u) || ((uintptr_t)b_scale & 3u))
+    return fail(QL_ERR_ALIGN, "a_scale and b_scale must be 4-byte aligned");
+  W4A4Params p{};
+  p.a = a_q4;
+  p.as = a_scale;
+  p.b = b_q4;
+  p.bs = b_scale;
+  p.bias = bias;
+  p.y = y;
+  p.M = (int)M;
+  p.N = (int)N;
+  p.K = (int)K;
+  p.out_dtype = out_dtype;
+  p.tiles_m = (int)((M + 127) / 128);
+  p.tiles_n = (int)((N + 127) / 128);
+  const hipError_t e = w4a4_launch(qblock, p, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(QL_ERR_LAUNCH, "w4a4 launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
 }  // extern "C"

@@ -84,6 +84,20 @@ hipError_t repack_q4_0_launch(const void* raw, void* packed, float* scale, int64
 hipError_t quantize_int8_per_token_launch(int dtype, const void* x, int8_t* q, float* scale,
                                           int64_t M, int64_t K, hipStream_t stream);
 
+// W4A4 GEMM with the reference's per-block fmaf accumulation (w4a4_gemm.hip).
+struct W4A4Params {
+  const void* a;         // [M, K/2] packed int4
+  const float* as;       // [M, K/qb]
+  const void* b;         // [N, K/2] packed int4
+  const float* bs;       // [N, K/qb]
+  const void* bias;      // [N] out dtype, or null
+  void* y;               // [M, N] out dtype
+  int M, N, K;
+  int out_dtype;
+  int tiles_m, tiles_n;  // 128 x 128 tiles
+};
+hipError_t w4a4_launch(int qblock, const W4A4Params& p, hipStream_t stream);
+
 // Fused DiT block glue (dit_fused.hip). K % 8 == 0 and K <= 16384 for the LayerNorm kernel;
 // head dim 128 for the q/k kernel; K % 8 == 0 for the residual.
 hipError_t adaln_to_f16_launch(int x_dtype, int mod_dtype, const void* x, const void* shift, const void* scale,

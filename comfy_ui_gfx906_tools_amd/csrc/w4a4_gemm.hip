@@ -1,0 +1,201 @@
+// W4A4 GEMM on gfx950 with the reference's production numerics (nodes/ComfyUI-Gfx906Int4/csrc/
+// int4_gemm_scaled.hip:53-191, gemm_int4 with splits = 1): A [M, K/2] and B [N, K/2] packed int4
+// (two's-complement nibbles, low nibble first), scales As [M, K/qb], Bs [N, K/qb] fp32, qb = 32 or
+// 16. For every quant block in K order: ip = exact int32 dot of the block's codes, then
+// acc = fmaf(float(ip), as * bs, acc); finally y = acc (+ bias) rounded to the output dtype.
+// The result is bit-identical to that sequence.
+//
+// * One quant block of 32 K is exactly the K of v_mfma_i32_16x16x32_i8, so each MFMA yields one
+//   block's integer dot for a 16 x 16 fragment (with qb = 16, two MFMAs per block, each with the
+//   other half's lanes zeroed). The nibbles go to the high half of each byte (code * 16): the
+//   MFMA returns 256 * ip exactly (|256 ip| <= 2^19), and the A scales are taken as as * 2^-8
+//   (exact), so fmaf(float(256 ip), (as * 2^-8) * bs, acc) rounds exactly like the reference's
+//   fmaf(float(ip), as * bs, acc) (the two products are the same real number).
+// * 128 x 128 tile per 256-thread workgroup, 4 waves as 2 x 2, each 64 x 64 = 4 x 4 fragments.
+//   A stage is 4 quant blocks (64 B of codes per row): global -> registers -> LDS, double
+//   buffered, one barrier per stage. In LDS a row keeps, per lane group j, the 4 dwords (one per
+//   block) that lane group j feeds to the MFMA, so a lane reads its operands for the whole stage
+//   with one 16-byte read; scales are stored block-major so a lane's 4 rows are one 16-byte read.
+// * Lane (r, j) of a fragment supplies row r and K slots 8j .. 8j+7 of the block, i.e. dword j of
+//   the row's 16-byte block (A and B use the same slot order, so the dot is unchanged); the
+//   accumulator lane layout is (row 4j + e, column r).
+#include "common.hpp"
+#include "launch.hpp"
+
+namespace qlinear {
+
+namespace {
+
+constexpr int kW4BM = 128, kW4BN = 128;
+constexpr int kW4StageBlocks = 4;                   // quant blocks of 32 K per stage
+constexpr int kW4RowBytes = kW4StageBlocks * 16;    // packed bytes per row per stage
+constexpr int kW4GroupM = 8;
+
+// 8 codes of a dword (K = 2t in the low nibble of byte t, 2t + 1 in the high one) as 8 int8 lanes
+// holding code * 16: low dword = even K, high dword = odd K.
+__device__ __forceinline__ long unpack_x16(uint32_t w) {
+  const uint32_t even = (w << 4) & 0xF0F0F0F0u;
+  const uint32_t odd = w & 0xF0F0F0F0u;
+  return (long)(((uint64_t)odd << 32) | even);
+}
+
+template <int SUB>
+__global__ __launch_bounds__(256) void w4a4_gemm_kernel(W4A4Params p) {
+  constexpr int kScaleCols = SUB * kW4StageBlocks;  // scale columns per stage
+  __shared__ __attribute__((aligned(16))) uint8_t lds_a[2][kW4BM * kW4RowBytes];
+  __shared__ __attribute__((aligned(16))) uint8_t lds_b[2][kW4BN * kW4RowBytes];
+  __shared__ __attribute__((aligned(16))) float lds_as[2][kScaleCols][kW4BM];
+  __shared__ __attribute__((aligned(16))) float lds_bs[2][kScaleCols][kW4BN];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int wm = wave >> 1, wn = wave & 1;
+  const int r16 = lane & 15, j4 = lane >> 4;
+  const int M = p.M, N = p.N, K = p.K;
+  const int KB = K / 32;                     // quant blocks of 32 along K
+  const int SC = KB * SUB;                   // scale columns per row
+  const int S = (KB + kW4StageBlocks - 1) / kW4StageBlocks;
+
+  const int g = xcd_remap(blockIdx.x, gridDim.x);
+  int tm, tn;
+  tile_coords(g, p.tiles_m, p.tiles_n, kW4GroupM, tm, tn);
+  const int m0 = tm * kW4BM, n0 = tn * kW4BN;
+  const uint8_t* A = (const uint8_t*)p.a;
+  const uint8_t* B = (const uint8_t*)p.b;
+  const size_t row_bytes = (size_t)K / 2;
+
+  // ---- stage loads: 512 16-byte chunks of A and of B (row c / 4, block c % 4), 128 x kScaleCols
+  //      scales of each ------------------------------------------------------------------------
+  u32x4 ra[2], rb[2];
+  float rsa[kScaleCols];
+  auto load_regs = [&](int s) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = tid + 256 * i, r = c >> 2, kb = s * kW4StageBlocks + (c & 3);
+      const bool ka = kb < KB;
+      ra[i] = (ka && m0 + r < M) ? *(const u32x4*)(A + (size_t)(m0 + r) * row_bytes + (size_t)kb * 16)
+                                 : u32x4{0u, 0u, 0u, 0u};
+      rb[i] = (ka && n0 + r < N) ? *(const u32x4*)(B + (size_t)(n0 + r) * row_bytes + (size_t)kb * 16)
+                                 : u32x4{0u, 0u, 0u, 0u};
+    }
+    // threads 0-127: A scales of row tid (taken as as * 2^-8); 128-255: B scales of row tid - 128
+    const int r = tid & 127;
+    const bool is_a = tid < 128;
+    const int gr = (is_a ? m0 : n0) + r;
+    const bool rok = gr < (is_a ? M : N);
+    const float* sp = is_a ? p.as : p.bs;
+#pragma unroll
+    for (int q = 0; q < kScaleCols; ++q) {
+      const int col = s * kScaleCols + q;
+      const float v = (rok && col < SC) ? sp[(size_t)gr * SC + col] : 0.0f;
+      rsa[q] = is_a ? v * 0.00390625f : v;
+    }
+  };
+  auto store_lds = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const int c = tid + 256 * i, r = c >> 2, b = c & 3;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const int off = r * kW4RowBytes + ((j ^ (r & 3)) << 4) + 4 * b;
+        *(uint32_t*)(lds_a[buf] + off) = ra[i][j];
+        *(uint32_t*)(lds_b[buf] + off) = rb[i][j];
+      }
+    }
+    const int r = tid & 127;
+    float(*dst)[kW4BM] = tid < 128 ? lds_as[buf] : lds_bs[buf];
+#pragma unroll
+    for (int q = 0; q < kScaleCols; ++q) dst[q][r] = rsa[q];
+  };
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int fm = 0; fm < 4; ++fm)
+#pragma unroll
+    for (int fn = 0; fn < 4; ++fn) acc[fm][fn] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  load_regs(0);
+  store_lds(0);
+  __syncthreads();
+  for (int s = 0; s < S; ++s) {
+    const int buf = s & 1;
+    if (s + 1 < S) load_regs(s + 1);
+    u32x4 a_raw[4], b_raw[4];
+#pragma unroll
+    for (int f = 0; f < 4; ++f) {
+      const int ra_row = wm * 64 + f * 16 + r16, rb_row = wn * 64 + f * 16 + r16;
+      a_raw[f] = *(const u32x4*)(lds_a[buf] + ra_row * kW4RowBytes + ((j4 ^ (ra_row & 3)) << 4));
+      b_raw[f] = *(const u32x4*)(lds_b[buf] + rb_row * kW4RowBytes + ((j4 ^ (rb_row & 3)) << 4));
+    }
+    const int nb = min(kW4StageBlocks, KB - s * kW4StageBlocks);  // uniform
+#pragma unroll
+    for (int b = 0; b < kW4StageBlocks; ++b) {
+      if (b >= nb) break;
+      long bop[4];
+#pragma unroll
+      for (int fn = 0; fn < 4; ++fn) bop[fn] = unpack_x16(b_raw[fn][b]);
+#pragma unroll
+      for (int sub = 0; sub < SUB; ++sub) {
+        long aop[4];
+#pragma unroll
+        for (int fm = 0; fm < 4; ++fm) {
+          const long v = unpack_x16(a_raw[fm][b]);
+          aop[fm] = (SUB == 1 || (j4 >> 1) == sub) ? v : 0l;  // qb = 16: K slots of this half only
+        }
+        i32x4 part[4][4];
+#pragma unroll
+        for (int fm = 0; fm < 4; ++fm)
+#pragma unroll
+          for (int fn = 0; fn < 4; ++fn)
+            part[fm][fn] = __builtin_amdgcn_mfma_i32_16x16x32_i8(aop[fm], bop[fn], i32x4{0, 0, 0, 0}, 0, 0, 0);
+        const int q = b * SUB + sub;
+        f32x4 sa[4];
+        float sb[4];
+#pragma unroll
+        for (int fm = 0; fm < 4; ++fm) sa[fm] = *(const f32x4*)&lds_as[buf][q][wm * 64 + fm * 16 + 4 * j4];
+#pragma unroll
+        for (int fn = 0; fn < 4; ++fn) sb[fn] = lds_bs[buf][q][wn * 64 + fn * 16 + r16];
+#pragma unroll
+        for (int fm = 0; fm < 4; ++fm)
+#pragma unroll
+          for (int fn = 0; fn < 4; ++fn)
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              acc[fm][fn][e] = __builtin_fmaf((float)part[fm][fn][e], sa[fm][e] * sb[fn], acc[fm][fn][e]);
+      }
+    }
+    if (s + 1 < S) store_lds(buf ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue: y = acc (+ bias), rounded once to the output dtype ----------------------------
+#pragma unroll
+  for (int fn = 0; fn < 4; ++fn) {
+    const int n = n0 + wn * 64 + fn * 16 + r16;
+    if (n >= N) continue;
+    const float bv = p.bias ? read_elem(p.bias, p.out_dtype, n) : 0.0f;
+#pragma unroll
+    for (int fm = 0; fm < 4; ++fm)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int m = m0 + wm * 64 + fm * 16 + 4 * j4 + e;
+        if (m >= M) continue;
+        float v = acc[fm][fn][e];
+        if (p.bias) v = v + bv;
+        write_elem(p.y, p.out_dtype, (size_t)m * N + n, v);
+      }
+  }
+}
+
+}  // namespace
+
+hipError_t w4a4_launch(int qblock, const W4A4Params& p, hipStream_t stream) {
+  const dim3 grid((unsigned)(p.tiles_m * p.tiles_n)), block(256);
+  if (qblock == 32)
+    hipLaunchKernelGGL(w4a4_gemm_kernel<1>, grid, block, 0, stream, p);
+  else
+    hipLaunchKernelGGL(w4a4_gemm_kernel<2>, grid, block, 0, stream, p);
+  return hipGetLastError();
+}
+
+}  // namespace qlinear

@@ -1,0 +1,47 @@
+"""The reference extension's Python surface for the int4 path (nodes/ComfyUI-Gfx906Int4/csrc/
+binding.cpp:52-112, 359-372: the module `_get_ext()` returns in ops.py:14-34), on libqlinear.so.
+
+    quantize_int4(x) -> (packed int8 [M, K/2], scale fp32 [M, K/32])
+    gemm_int4(A_packed, A_scale, B_packed, B_scale, bias, out_dtype, splits=0, qblock=32)
+    gemm_int4_auto_splits(M, N, K)
+
+Same argument meaning, shapes and error behaviour (RuntimeError naming expected vs actual), so
+the reference's own `int4_linear` -- ext.quantize_int4 then ext.gemm_int4 (ops.py:181-182), its
+W4A4 production path -- runs unchanged on MI355X with bit-identical results to its unsplit run:
+the activation quantizer follows the reference kernel's rule (scale = amax * (1/7), rint) and the
+GEMM its per-block fmaf order. `splits` is accepted for compatibility; the MI355X kernel never
+cuts K (the reference's split-K adds per-split fp32 partials, another association of the same
+sum), so gemm_int4_auto_splits returns 1. The block-32 int8 functions of the reference extension
+(quantize_int8 / gemm_int8 / conv_int8, used by its VAE and training nodes) are not provided.
+"""
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+MAX_SPLITS = 8  # binding.cpp: splits in [0, MAX_SPLITS]
+
+
+def quantize_int4(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """x [M, K] float32/16/bf16 on the GPU, K % 32 == 0 -> (packed int8 [M, K/2], scale fp32 [M, K/32])."""
+    if not (isinstance(x, torch.Tensor) and x.is_cuda):
+        raise RuntimeError("x must be on device")
+    if x.dim() != 2 or x.shape[1] % 32 != 0:
+        raise RuntimeError(f"x must be [M, K] with K % 32 == 0, got {list(x.shape)}")
+    return _lib.quantize_int4(x, rule=_lib.RULE_RECIP)
+
+
+def gemm_int4(A_packed: torch.Tensor, A_scale: torch.Tensor, B_packed: torch.Tensor, B_scale: torch.Tensor,
+              bias: torch.Tensor | None, out_dtype: torch.dtype, splits: int = 0, qblock: int = 32) -> torch.Tensor:
+    """[M, N] in out_dtype = block-scaled int4 A [M, K/2] x B [N, K/2]^T (+ bias in out_dtype)."""
+    if not (A_packed.is_cuda and B_packed.is_cuda):
+        raise RuntimeError("inputs must be on device")
+    if not 0 <= int(splits) <= MAX_SPLITS:
+        raise RuntimeError(f"splits must be in [0, {MAX_SPLITS}], got {splits}")
+    return _lib.w4a4_gemm(A_packed, A_scale, B_packed, B_scale, bias, out_dtype=out_dtype, qblock=int(qblock))
+
+
+def gemm_int4_auto_splits(M: int, N: int, K: int) -> int:
+    """Split-K count gemm_int4 uses for [M, K] x [N, K]^T: always 1 here (no K cut)."""
+    return 1

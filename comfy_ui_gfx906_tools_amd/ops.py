@@ -32,9 +32,12 @@ _ROTATION_CACHE: dict = {}
 
 
 def _get_ext():
-    """The native library (ctypes handle); raises if it was not built. Mirrors ops.py:17-34,
-    which JIT-built a pybind11 extension instead."""
-    return _lib.load_library()
+    """The extension module of the int4 path (quantize_int4 / gemm_int4 / gemm_int4_auto_splits,
+    comfy_ui_gfx906_tools_amd.ext) with libqlinear.so loaded; raises if the library was not built.
+    Mirrors ops.py:14-34, which JIT-built a pybind11 extension instead."""
+    _lib.load_library()
+    from . import ext
+    return ext
 
 
 # ---------------------------------------------------------------------------------------------
@@ -147,6 +150,23 @@ def int4_linear(x: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.Tensor, 
         R = get_group_rotation(K, rotation_group, x2d.device)
         x2d = apply_group_rotation(x2d.float(), R, rotation_group)
     out = _lib.w4a16_gemm(x2d, w_packed, w_scale, bias, out_dtype=x.dtype)
+    return out.reshape(*shape[:-1], w_packed.shape[0])
+
+
+def int4_linear_w4a4(x: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.Tensor, bias: torch.Tensor | None = None,
+                     rotation_group: int = 0) -> torch.Tensor:
+    """The reference's own int4_linear (ops.py:167-183): x is quantized to block-32 int4 as well
+    (W4A4) and multiplied by the block-scaled int4 GEMM; bit-identical to the reference's unsplit
+    run on the same inputs. int4_linear (W4A16) is the engine's default path."""
+    ext = _get_ext()
+    shape = x.shape
+    K = shape[-1]
+    x2d = x.reshape(-1, K)
+    if rotation_group:
+        R = get_group_rotation(K, rotation_group, x2d.device)
+        x2d = apply_group_rotation(x2d.float(), R, rotation_group)
+    qa, sa = ext.quantize_int4(x2d.contiguous())
+    out = ext.gemm_int4(qa, sa, w_packed, w_scale, bias, x.dtype)
     return out.reshape(*shape[:-1], w_packed.shape[0])
 
 

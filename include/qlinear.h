@@ -152,6 +152,20 @@ int qlinear_w8a8_gemm(int out_dtype, const int8_t* xq, const float* x_scale, con
                       int64_t K, void* stream);
 
 /* ---------------------------------------------------------------------------------------
+ * W4A4 linear with the reference's production numerics: a_q4 [M, K/2] (activations from
+ * qlinear_quantize_int4, rule 1) and b_q4 [N, K/2] packed int4, scales a_scale [M, K/qblock],
+ * b_scale [N, K/qblock] fp32, qblock 32 or 16. For each quant block in K order:
+ *   ip = exact int32 dot of the block's codes; acc = fmaf(float(ip), a_scale * b_scale, acc)
+ * then y = acc (+ bias) rounded once to out_dtype (bias of dtype out_dtype): bit-identical to
+ * gemm_dispatch (csrc/int4_gemm_scaled.hip:254-269, kernel :53-191) run unsplit (splits = 1;
+ * its split-K runs add per-split fp32 partials, a different association). Counterpart of
+ * ext.gemm_int4 (csrc/binding.cpp:70-112). K % 32 == 0; a_q4, b_q4 16-byte aligned.
+ * ------------------------------------------------------------------------------------- */
+int qlinear_w4a4_gemm(int out_dtype, const void* a_q4, const float* a_scale, const void* b_q4,
+                      const float* b_scale, const void* bias, void* y, int64_t M, int64_t N,
+                      int64_t K, int qblock, void* stream);
+
+/* ---------------------------------------------------------------------------------------
  * Fused DiT block glue. No counterpart in the reference: its node patches only the Linears of
  * ComfyUI's Flux model (nodes/ComfyUI-Gfx906Int4/nodes.py:71-124, 447-599) and the layer norms,
  * modulation, QK-norm, RoPE and gated residuals run as separate torch ops around them. Each entry

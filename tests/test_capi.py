@@ -139,6 +139,18 @@ def test_quantizer_and_w8a8_argument_checks(lib):
     assert lib.qlinear_rows_to_f16(3, None, None, None, 4, 16, None) == QL_ERR_DTYPE
 
 
+def test_w4a4_entry_point_checks_arguments(lib):
+    p16 = ctypes.c_void_p(256)
+    f = lib.qlinear_w4a4_gemm
+    assert f(3, None, None, None, None, None, None, 4, 64, 64, 32, None) == QL_ERR_DTYPE
+    assert f(0, None, None, None, None, None, None, 4, 64, 64, 8, None) == QL_ERR_ARG
+    assert f(0, None, None, None, None, None, None, 4, 64, 48, 32, None) == QL_ERR_SHAPE
+    assert f(0, None, None, None, None, None, None, 0, 64, 64, 32, None) == QL_OK
+    assert f(0, None, None, None, None, None, None, 4, 64, 64, 32, None) == QL_ERR_ARG
+    assert f(0, ctypes.c_void_p(264), p16, p16, p16, None, p16, 4, 64, 64, 16, None) == QL_ERR_ALIGN
+    assert f(0, p16, ctypes.c_void_p(258), p16, p16, None, p16, 4, 64, 64, 16, None) == QL_ERR_ALIGN
+
+
 def test_fused_dit_entry_points_check_arguments(lib):
     """The fused DiT glue entry points reject bad arguments before any launch."""
     p16 = ctypes.c_void_p(256)
