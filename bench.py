@@ -12,12 +12,14 @@ dequant-then-matmul path on the host cores).
 
 Usage: python bench.py [--gpus 1] [--steps 20] [--warmup 5] [--no-cpu-baseline]
 
-`--workload c3` and `--workload c4` instead measure the other BASELINE configurations (one JSON
-line each, not the driver's line): C3 = the W8A8 linear 3072 -> 21504 at M = 4608 (per-token int8
-quantize + int8 GEMM, bf16 out) against the int8 MFMA peak; C4 = the skinny-M sweep (W4A16 at
-K = 4096, N = 10240 for M in {1, 4, 16, 64, 256}, plus 3072 -> 18432 at M = 1) against the HBM
-peak, with 12 weight copies in rotation (more than the 256 MB last-level cache) and the calls
-replayed back to back from a HIP graph.
+`--workload c1 | c3 | c4 | c5` instead measure the other BASELINE configurations (one JSON line
+each, not the driver's line): C1 = the single linear x fp16 [4608, 3072] x W [3072, 3072] (W4A16,
+and the reference's W4A4 numerics on the same shape); C3 = the W8A8 linear 3072 -> 21504 at
+M = 4608 (per-token int8 quantize + int8 GEMM, bf16 out) against the int8 MFMA peak; C4 = the
+skinny-M sweep (W4A16 at K = 4096, N = 10240 for M in {1, 4, 16, 64, 256}, plus 3072 -> 18432 at
+M = 1) against the HBM peak, with 12 weight copies in rotation (more than the 256 MB last-level
+cache) and the calls replayed back to back from a HIP graph; C5 = one denoise step of the 12B
+Flux-style DiT with every Linear on the engine (ms/step).
 """
 from __future__ import annotations
 
@@ -40,7 +42,7 @@ def parse():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--cpu-repeats", type=int, default=3)
-    ap.add_argument("--workload", choices=["c2", "c3", "c4", "c5"], default="c2")
+    ap.add_argument("--workload", choices=["c1", "c2", "c3", "c4", "c5"], default="c2")
     ap.add_argument("--calibrate-copy", action="store_true",
                     help="only run a plain 1 GiB device copy three times (reference kernel for the "
                          "FETCH_SIZE / WRITE_SIZE counters) and exit")
@@ -110,6 +112,9 @@ def main():
         return
     if args.workload == "c5":
         bench_c5(args)
+        return
+    if args.workload == "c1":
+        bench_c1(args)
         return
     import numpy as np
     import torch
@@ -346,6 +351,84 @@ def bench_c4(args):
                       "dtype": "int4 weights, bf16 activations", "data": "synthetic",
                       "timing": "HIP graph of 48 calls over 12 weight copies, replayed back to back",
                       "results": res}), flush=True)
+
+
+def bench_c1(args):
+    """C1: the single linear of BASELINE config 1 -- x fp16 [4608, 3072] ~ N(0, 1), W [3072, 3072]
+    ~ N(0, 0.02) quantized to int4 group 32 with fp16-representable scales (amax / 7 rounded to
+    fp16, stored in the fp32 scale layout), seed 0. Two GPU paths, each timed with HIP events over
+    `steps` calls: the engine's W4A16 GEMM (fp16 x straight into fp16 MFMA), gated at 2e-3 against
+    the fp32 dequant-then-matmul, and the reference's own W4A4 numerics (activation quantize_int4 +
+    the W4A4 GEMM), checked bit-exact against the oracle on rows at both ends. CPU baseline: the
+    oracle's fp32 dequant-then-matmul of the whole call on the host."""
+    import numpy as np
+    import torch
+    sys.path.insert(0, HERE)
+    from comfy_ui_gfx906_tools_amd import _lib, ext
+    from oracle import qlinear_oracle as orc
+    M, K, N = 4608, 3072, 3072
+    torch.cuda.set_device(0)
+    _lib.load_library()
+    g = torch.Generator().manual_seed(0)
+    x = torch.randn(M, K, generator=g).to(torch.float16)
+    w = torch.randn(N, K, generator=g) * 0.02
+    wb = w.numpy().reshape(N, K // 32, 32)
+    s16 = (np.abs(wb).max(-1).clip(min=1e-8) / np.float32(7)).astype(np.float16).astype(np.float32)
+    codes = np.clip(np.rint(wb / s16[..., None]), -8, 7).astype(np.int32).reshape(N, K)
+    wq = ((codes[:, 0::2] & 0xF) | ((codes[:, 1::2] & 0xF) << 4)).astype(np.uint8).view(np.int8)
+    xd, wqd, wsd = x.cuda(), torch.from_numpy(wq).cuda(), torch.from_numpy(s16).cuda()
+
+    def timed(fn):
+        for _ in range(args.warmup):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            out = fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return out, e0.elapsed_time(e1) / args.steps
+
+    y16, ms16 = timed(lambda: _lib.w4a16_gemm(xd, wqd, wsd, None, out_dtype=torch.float16))
+    y32 = _lib.w4a16_gemm(xd, wqd, wsd, None, out_dtype=torch.float32)
+    ref = xd.float() @ dequant_fp32(wqd, wsd).t()
+    err = ((y32 - ref).abs().max() / ref.abs().max()).item()
+    (qa, sa), ms_q = timed(lambda: ext.quantize_int4(xd))
+    y44, ms44 = timed(lambda: ext.gemm_int4(*ext.quantize_int4(xd), wqd, wsd, None, torch.float16))
+    _, ms44g = timed(lambda: ext.gemm_int4(qa, sa, wqd, wsd, None, torch.float16))
+    y44f = ext.gemm_int4(qa, sa, wqd, wsd, None, torch.float32).cpu().numpy()
+    qa_np, sa_np = qa.cpu().numpy(), sa.cpu().numpy()
+    exact = all(np.array_equal(y44f[r], orc.gemm_int4_w4a4(qa_np[r], sa_np[r], wq, s16)) for r in
+                (slice(0, 32), slice(M - 32, M)))
+    flops = 2.0 * M * N * K
+    out = {"metric": "W4A16 GEMM TFLOP/s at the C1 shape (x fp16 [4608, 3072], W [3072, 3072] int4 g32)",
+           "value": round(flops / (ms16 * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": round(ms16, 4), "higher_is_better": True, "dtype": "f16",
+           "data": "synthetic, seed 0", "config": {"workload": "C1 single W4A16 linear, fp16 out"},
+           "roofline": {"bound": "mfma", "achieved": round(flops / (ms16 * 1e-3) / 1e12, 2),
+                        "peak": PEAK_BF16_TFLOPS, "unit": "TFLOP/s",
+                        "frac": round(flops / (ms16 * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4)},
+           "parity": {"w4a16_fp32_max_rel_err": err, "gate": GATE, "pass": bool(err <= GATE)},
+           "w4a4_reference_numerics": {
+               "tops_with_quantize": round(flops / (ms44 * 1e-3) / 1e12, 2),
+               "tops_gemm_only": round(flops / (ms44g * 1e-3) / 1e12, 2), "ms_gemm": round(ms44g, 4),
+               "ms_quantize": round(ms_q, 4),
+               "int8_peak_frac_gemm": round(flops / (ms44g * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4),
+               "bit_exact_rows_vs_oracle": bool(exact)}}
+    if not args.no_cpu_baseline:
+        threads = torch.get_num_threads()
+        wd = orc.dequant_int4(wq, s16)
+        xf = x.float().numpy()
+        best = float("inf")
+        for _ in range(max(1, args.cpu_repeats)):
+            t0 = time.perf_counter()
+            _ = xf @ wd.T
+            best = min(best, time.perf_counter() - t0)
+        out["cpu_baseline"] = {"value": round(flops / best / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
+                               "kind": "port", "sample": f"whole C1 call, fp32 numpy BLAS on the host, dequant outside "
+                                                         f"the timing, best of {args.cpu_repeats}: {best:.3f} s"}
+    print(json.dumps(out), flush=True)
 
 
 def bench_c5(args):
