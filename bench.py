@@ -401,6 +401,14 @@ def bench_c1(args):
     qa_np, sa_np = qa.cpu().numpy(), sa.cpu().numpy()
     exact = all(np.array_equal(y44f[r], orc.gemm_int4_w4a4(qa_np[r], sa_np[r], wq, s16)) for r in
                 (slice(0, 32), slice(M - 32, M)))
+    # a rotated layer (activation_rotation=True checkpoints): group-128 Hadamard rotation of x fused
+    # into the fp16 staging pass, against the unfused sequence (fp32 rotation matmul, fp32 staging)
+    from comfy_ui_gfx906_tools_amd import ops
+    grp = ops.choose_rotation_group(K)
+    _, ms_rot = timed(lambda: ops.int4_linear(xd, wqd, wsd, None, rotation_group=grp))
+    R = ops.get_group_rotation(K, grp, xd.device)
+    _, ms_rot_unfused = timed(lambda: _lib.w4a16_gemm(ops.apply_group_rotation(xd.float(), R, grp), wqd, wsd, None,
+                                                      out_dtype=torch.float16))
     flops = 2.0 * M * N * K
     out = {"metric": "W4A16 GEMM TFLOP/s at the C1 shape (x fp16 [4608, 3072], W [3072, 3072] int4 g32)",
            "value": round(flops / (ms16 * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
@@ -415,7 +423,9 @@ def bench_c1(args):
                "tops_gemm_only": round(flops / (ms44g * 1e-3) / 1e12, 2), "ms_gemm": round(ms44g, 4),
                "ms_quantize": round(ms_q, 4),
                "int8_peak_frac_gemm": round(flops / (ms44g * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4),
-               "bit_exact_rows_vs_oracle": bool(exact)}}
+               "bit_exact_rows_vs_oracle": bool(exact)},
+           "rotated_layer_group128": {"ms_fused": round(ms_rot, 4), "ms_unfused": round(ms_rot_unfused, 4),
+                                      "tflops_fused": round(flops / (ms_rot * 1e-3) / 1e12, 2)}}
     if not args.no_cpu_baseline:
         threads = torch.get_num_threads()
         wd = orc.dequant_int4(wq, s16)

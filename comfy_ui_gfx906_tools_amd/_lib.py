@@ -58,6 +58,7 @@ SIGNATURES = {
                                       _c_i64, _c_i64, _c_i64, ctypes.c_float, _c_vp]),
     "qlinear_w4a4_gemm": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int,
                                    _c_vp]),
+    "qlinear_rotate_rows_to_f16": (_c_int, [_c_int, _c_vp, _c_vp, _c_int, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
     "qlinear_gated_residual": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
 }
 
@@ -313,6 +314,26 @@ def w8a8_gemm(xq: torch.Tensor, x_scale: torch.Tensor, wq: torch.Tensor, w_scale
                                    _stream_ptr(xq.device))
     _check(rc, "w8a8_gemm")
     return y
+
+
+def rotate_rows_to_f16(x: torch.Tensor, signs: torch.Tensor, group: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """Per-group rotation x_g -> H (signs * x_g) / sqrt(group) of x [M, K], written as the W4A16
+    GEMM's fp16 operand: (x16 [M, K] fp16, row_scale [M] fp32)."""
+    lib = load_library()
+    x = _dev_tensor(x, "x")
+    signs = _dev_tensor(signs, "signs").float().reshape(-1)
+    if x.dim() != 2 or x.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        raise RuntimeError(f"x must be a float32/float16/bfloat16 [M, K] tensor, got {x.dtype} {tuple(x.shape)}")
+    if signs.numel() != group:
+        raise RuntimeError(f"signs must have {group} elements, got {signs.numel()}")
+    M, K = x.shape
+    x16 = torch.empty((M, K), dtype=torch.float16, device=x.device)
+    rs = torch.empty((M,), dtype=torch.float32, device=x.device)
+    with torch.cuda.device(x.device):
+        rc = lib.qlinear_rotate_rows_to_f16(_DTYPE_CODE[x.dtype], x.data_ptr(), signs.data_ptr(), int(group),
+                                            x16.data_ptr(), rs.data_ptr(), M, K, _stream_ptr(x.device))
+    _check(rc, "rotate_rows_to_f16")
+    return x16, rs
 
 
 def w4a4_gemm(a_q4: torch.Tensor, a_scale: torch.Tensor, b_q4: torch.Tensor, b_scale: torch.Tensor,

@@ -526,4 +526,23 @@ int qlinear_w4a4_gemm(int out_dtype, const void* a_q4, const float* a_scale, con
   return ok();
 }
 
+int qlinear_rotate_rows_to_f16(int x_dtype, const void* x, const float* signs, int group, void* x16, float* row_scale,
+                               int64_t M, int64_t K, void* stream) {
+  if (x_dtype != QL_F32 && x_dtype != QL_F16 && x_dtype != QL_BF16)
+    return fail(QL_ERR_DTYPE, "x dtype %s (%d) unsupported, expected float32/float16/bfloat16", dtype_name(x_dtype),
+                x_dtype);
+  if (group != 32 && group != 64 && group != 128)
+    return fail(QL_ERR_ARG, "rotation group must be 32, 64 or 128, got %d", group);
+  if (M < 0 || M > INT32_MAX || K <= 0 || K % group != 0 || K > 16384)
+    return fail(QL_ERR_SHAPE, "x must be [M, K] with K %% %d == 0 and K <= 16384, got [%lld, %lld]", group,
+                (long long)M, (long long)K);
+  if (M == 0) return ok();
+  if (!x || !signs || !x16 || !row_scale) return fail(QL_ERR_ARG, "null x / signs / x16 / row_scale pointer");
+  if (!aligned16(x) || !aligned16(x16)) return fail(QL_ERR_ALIGN, "x and x16 must be 16-byte aligned");
+  if ((uintptr_t)signs & 3u) return fail(QL_ERR_ALIGN, "signs must be 4-byte aligned");
+  const hipError_t e = rotate_rows_to_f16_launch(x_dtype, group, x, signs, x16, row_scale, M, K, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(QL_ERR_LAUNCH, "rotate_rows_to_f16 launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
 }  // extern "C"

@@ -98,6 +98,11 @@ struct W4A4Params {
 };
 hipError_t w4a4_launch(int qblock, const W4A4Params& p, hipStream_t stream);
 
+// Activation rotation + fp16 staging in one pass (rotate.hip): group 32 / 64 / 128, K % group == 0,
+// K <= 16384.
+hipError_t rotate_rows_to_f16_launch(int x_dtype, int group, const void* x, const float* signs, void* x16,
+                                     float* row_scale, int64_t M, int64_t K, hipStream_t stream);
+
 // Fused DiT block glue (dit_fused.hip). K % 8 == 0 and K <= 16384 for the LayerNorm kernel;
 // head dim 128 for the q/k kernel; K % 8 == 0 for the residual.
 hipError_t adaln_to_f16_launch(int x_dtype, int mod_dtype, const void* x, const void* shift, const void* scale,

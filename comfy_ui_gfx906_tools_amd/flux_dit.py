@@ -24,7 +24,8 @@ import torch
 import torch.nn.functional as F
 
 from . import _lib
-from .ops import Gfx906Int4Ops, apply_group_rotation, get_group_rotation, quantize_pack_int4
+from .ops import (ROTATE_FUSED_MAX_K, Gfx906Int4Ops, apply_group_rotation, get_group_rotation, get_group_signs,
+                  quantize_pack_int4)
 
 
 @dataclass(frozen=True)
@@ -110,10 +111,15 @@ def _linear(layer, x, gelu: bool = False, rows: slice | None = None) -> torch.Te
             return y.reshape(*x.lead, wq.shape[0])
         shape = x.shape
         x2 = x.reshape(-1, shape[-1])
+        bias = b.to(x.dtype) if b is not None else None
         if layer.rotation_group:  # the weight was folded through the rotation (as int4_linear does)
             g = layer.rotation_group
+            if shape[-1] <= ROTATE_FUSED_MAX_K:
+                x16, rs = _lib.rotate_rows_to_f16(x2, get_group_signs(g, x2.device), g)
+                y = _lib.w4a16_gemm(x16, wq, ws, bias, out_dtype=x.dtype, row_scale=rs, gelu=gelu)
+                return y.reshape(*shape[:-1], wq.shape[0])
             x2 = apply_group_rotation(x2.float(), get_group_rotation(shape[-1], g, x2.device), g)
-        y = _lib.w4a16_gemm(x2, wq, ws, b.to(x.dtype) if b is not None else None, out_dtype=x.dtype, gelu=gelu)
+        y = _lib.w4a16_gemm(x2, wq, ws, bias, out_dtype=x.dtype, gelu=gelu)
         return y.reshape(*shape[:-1], wq.shape[0])
     w, b = layer.weight, layer.bias
     if rows is not None:

@@ -22,6 +22,7 @@ from . import _lib
 
 BLOCK = 32  # ops.py:196
 ROTATION_SEED = 0  # ops.py:39: weight-fold time and forward time must agree
+ROTATE_FUSED_MAX_K = 16384  # the fused rotation + staging kernel keeps a row in registers
 
 # Which scale rule torch's own `amax / 7.0` follows on each device (see _lib.RULE_*): the HIP
 # quantizer reproduces torch's result on the device the weight lives on.
@@ -80,6 +81,17 @@ def get_group_rotation(in_features: int, group: int, device) -> torch.Tensor:
         r = _hadamard(group, device) * signs.to(device)
         _ROTATION_CACHE[key] = r
     return r
+
+
+def get_group_signs(group: int, device) -> torch.Tensor:
+    """The +-1 column signs of get_group_rotation (fp32 [group]): R = H * signs, and the first
+    row of the Sylvester H is all ones, so they are R's first row times sqrt(group)."""
+    key = ("signs", group, torch.device(device))
+    s = _ROTATION_CACHE.get(key)
+    if s is None:
+        s = torch.sign(get_group_rotation(group, group, device)[0]).contiguous()
+        _ROTATION_CACHE[key] = s
+    return s
 
 
 def apply_group_rotation(t: torch.Tensor, R: torch.Tensor, group: int) -> torch.Tensor:
@@ -146,6 +158,11 @@ def int4_linear(x: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.Tensor, 
     shape = x.shape
     K = shape[-1]
     x2d = x.reshape(-1, K)
+    if rotation_group and x2d.is_cuda and K <= ROTATE_FUSED_MAX_K:
+        # rotation and fp16 staging in one pass, then the GEMM on the staged operand
+        x16, rs = _lib.rotate_rows_to_f16(x2d, get_group_signs(rotation_group, x2d.device), rotation_group)
+        out = _lib.w4a16_gemm(x16, w_packed, w_scale, bias, out_dtype=x.dtype, row_scale=rs)
+        return out.reshape(*shape[:-1], w_packed.shape[0])
     if rotation_group:
         R = get_group_rotation(K, rotation_group, x2d.device)
         x2d = apply_group_rotation(x2d.float(), R, rotation_group)

@@ -108,6 +108,15 @@ int qlinear_rows_to_f16(int x_dtype, const void* x, void* x16, float* row_scale,
  * ext.gemm_int4_auto_splits (csrc/binding.cpp:36-43, 359-362). */
 int qlinear_w4a16_auto_splits(int64_t M, int64_t N, int64_t K, int device);
 
+/* Rotated fp16 staging: per row, every group of `group` (32, 64 or 128) elements along K becomes
+ * y_g = H (signs * x_g) / sqrt(group) (Sylvester Hadamard H; signs fp32 +-1 [group]), i.e.
+ * x_g R^T with R = H diag(signs) / sqrt(group), then is written as qlinear_rows_to_f16 writes
+ * (x16 = y * 2^-e_m, row_scale[m] = 2^e_m; pass both to qlinear_w4a16_gemm with x_dtype QL_F16).
+ * Replaces the fp32 activation rotation of a rotated layer's forward (ops.py:176-179,
+ * apply_group_rotation ops.py:85-105) plus the staging pass. K % group == 0, K <= 16384. */
+int qlinear_rotate_rows_to_f16(int x_dtype, const void* x, const float* signs, int group, void* x16,
+                               float* row_scale, int64_t M, int64_t K, void* stream);
+
 /* ---------------------------------------------------------------------------------------
  * Symmetric block-32 int4 quantize + pack of a float matrix x[rows, K] (fp32/fp16/bf16):
  *   scale = max(amax(block), 1e-8) / 7      (rule 0, torch on CPU: ops.py:115-116)
