@@ -59,6 +59,8 @@ SIGNATURES = {
     "qlinear_w4a4_gemm": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int,
                                    _c_vp]),
     "qlinear_rotate_rows_to_f16": (_c_int, [_c_int, _c_vp, _c_vp, _c_int, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
+    "qlinear_heads_to_f16": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp,
+                                      _c_vp, _c_vp]),
     "qlinear_gated_residual": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
 }
 
@@ -462,3 +464,30 @@ def gated_residual(x: torch.Tensor, gate: torch.Tensor, y: torch.Tensor, out: to
                                         y.data_ptr(), x.numel() // K if K else 0, K, _stream_ptr(x.device))
     _check(rc, "gated_residual")
     return out
+
+
+def heads_to_f16(o: torch.Tensor, l_offset: int = 0, rows: int | None = None,
+                 extra: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """Rows [l_offset, l_offset + rows) of an attention output o [H, L, 128] flattened over heads,
+    each followed by the same row of `extra` [rows, E], as the W4A16 GEMM's fp16 operand:
+    (x16 [rows, H * 128 + E] fp16, row_scale [rows] fp32)."""
+    lib = load_library()
+    o = _dev_tensor(o, "o")
+    if o.dim() != 3 or o.shape[2] != 128 or o.dtype not in (torch.bfloat16, torch.float16):
+        raise RuntimeError(f"o must be a bfloat16/float16 [H, L, 128] tensor, got {o.dtype} {tuple(o.shape)}")
+    H, L = o.shape[0], o.shape[1]
+    rows = L - l_offset if rows is None else rows
+    E = 0
+    if extra is not None:
+        extra = _dev_tensor(extra, "extra")
+        if extra.dtype != o.dtype or extra.dim() != 2 or extra.shape[0] != rows:
+            raise RuntimeError(f"extra must be a {o.dtype} [{rows}, E] tensor, got {extra.dtype} {tuple(extra.shape)}")
+        E = extra.shape[1]
+    x16 = torch.empty((rows, H * 128 + E), dtype=torch.float16, device=o.device)
+    rs = torch.empty((rows,), dtype=torch.float32, device=o.device)
+    with torch.cuda.device(o.device):
+        rc = lib.qlinear_heads_to_f16(_DTYPE_CODE[o.dtype], o.data_ptr(), H, L, 128, l_offset, rows,
+                                      extra.data_ptr() if extra is not None else None, E, x16.data_ptr(),
+                                      rs.data_ptr(), _stream_ptr(o.device))
+    _check(rc, "heads_to_f16")
+    return x16, rs

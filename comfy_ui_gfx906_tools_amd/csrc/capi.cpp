@@ -545,4 +545,24 @@ int qlinear_rotate_rows_to_f16(int x_dtype, const void* x, const float* signs, i
   return ok();
 }
 
+int qlinear_heads_to_f16(int dtype, const void* o, int64_t H, int64_t L_all, int64_t D, int64_t l_offset, int64_t rows,
+                         const void* extra, int64_t E, void* x16, float* row_scale, void* stream) {
+  if (dtype != QL_F16 && dtype != QL_BF16)
+    return fail(QL_ERR_DTYPE, "dtype %s (%d) unsupported, expected float16/bfloat16", dtype_name(dtype), dtype);
+  if (D != 128) return fail(QL_ERR_SHAPE, "head dim must be 128, got %lld", (long long)D);
+  if (H <= 0 || rows < 0 || l_offset < 0 || l_offset + rows > L_all || L_all > INT32_MAX || E < 0 || E % 8 != 0 ||
+      H * 128 + E > 16384)
+    return fail(QL_ERR_SHAPE, "expected o [H, L_all, 128] rows [l_offset, l_offset + rows) and extra [rows, E] with "
+                "E %% 8 == 0, H * 128 + E <= 16384; got H=%lld L_all=%lld l_offset=%lld rows=%lld E=%lld", (long long)H,
+                (long long)L_all, (long long)l_offset, (long long)rows, (long long)E);
+  if (rows == 0) return ok();
+  if (!o || !x16 || !row_scale || (E > 0 && !extra)) return fail(QL_ERR_ARG, "null o / extra / x16 / row_scale pointer");
+  if (!aligned16(o) || !aligned16(x16) || (E > 0 && !aligned16(extra)))
+    return fail(QL_ERR_ALIGN, "o, extra and x16 must be 16-byte aligned");
+  const hipError_t e = heads_to_f16_launch(dtype, o, H, L_all, l_offset, rows, E > 0 ? extra : nullptr, E, x16,
+                                           row_scale, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(QL_ERR_LAUNCH, "heads_to_f16 launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
 }  // extern "C"

@@ -8,6 +8,9 @@
 //  * qk_norm_rope_kernel: splits a qkv projection [L, 3, H, D] into q, k, v [H, L_out, D] at row
 //    offset l0, with RMSNorm over D (learned scale) and the RoPE pair rotation on q and k.
 //  * gated_residual_kernel: out = x + gate * y with gate broadcast over rows.
+//  * heads_to_f16_kernel: rows of an attention output in the head-major layout [H, L, D], optionally
+//    followed by the same row of a second [L, E] tensor, gathered into the row-scaled fp16 operand
+//    of the next GEMM (the head transpose, a concatenation and the staging pass in one).
 //
 // Every value is computed in fp32 and rounded once to the output type.
 #include "common.hpp"
@@ -205,6 +208,50 @@ __global__ __launch_bounds__(256) void gated_residual_kernel(void* out, const vo
   }
 }
 
+// One 256-thread block per output row l; thread t holds row elements 8t + 2048 r (r < R): element
+// p < H * 128 is o[p / 128, l0 + l, p % 128], element p >= H * 128 is extra[l, p - H * 128].
+template <int DT, int R>
+__global__ __launch_bounds__(256) void heads_to_f16_kernel(const void* __restrict__ o, const void* __restrict__ extra,
+                                                           _Float16* __restrict__ x16, float* __restrict__ row_scale,
+                                                           int H, int L_all, int l0, int E) {
+  constexpr int D = 128;
+  __shared__ float red[4];
+  const int l = blockIdx.x;
+  const int HD = H * D, Kt = HD + E;
+  float v[R][8];
+  float amax = 0.0f;
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int p = threadIdx.x * 8 + r * 2048;
+    if (p < Kt) {
+      if (p < HD)
+        load8<DT>(o, ((size_t)(p / D) * L_all + (size_t)(l0 + l)) * D + (p % D), v[r]);
+      else
+        load8<DT>(extra, (size_t)l * E + (p - HD), v[r]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[r][e]));
+    }
+  }
+  amax = block_max(amax, red);
+  int ex = 0;
+  if (amax > 0.0f && amax <= 3.0e38f) {
+    int E2;
+    frexpf(amax, &E2);  // amax = f * 2^E2, f in [0.5, 1)
+    ex = E2 - 15;
+  }
+  if (threadIdx.x == 0) row_scale[l] = ldexpf(1.0f, ex);
+#pragma unroll
+  for (int r = 0; r < R; ++r) {
+    const int p = threadIdx.x * 8 + r * 2048;
+    if (p < Kt) {
+      float q[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) q[e] = ldexpf(v[r][e], -ex);
+      store8<kF16>(x16, (size_t)l * Kt + p, q);
+    }
+  }
+}
+
 template <int XDT, int MDT>
 hipError_t adaln_launch_r(const void* x, const void* shift, const void* scale, void* x16, float* rs, int64_t M,
                           int64_t K, float eps, hipStream_t st) {
@@ -257,6 +304,32 @@ hipError_t qk_norm_rope_launch(int dtype, const void* qkv, const void* q_norm, c
     hipLaunchKernelGGL(qk_norm_rope_kernel<kF16>, grid, block, 0, stream, qkv, q_norm, k_norm, cosv, sinv, q, k, v,
                        (int)L, (int)H, (int)L_out, (int)l0, eps);
   return hipGetLastError();
+}
+
+template <int DT>
+static hipError_t heads_launch_r(const void* o, const void* extra, void* x16, float* rs, int64_t H, int64_t L_all,
+                                 int64_t l0, int64_t rows, int64_t E, hipStream_t st) {
+  const int64_t Kt = H * 128 + E;
+  const dim3 grid((unsigned)rows), block(256);
+#define QL_HEADS(R)                                                                                         \
+  hipLaunchKernelGGL((heads_to_f16_kernel<DT, R>), grid, block, 0, st, o, extra, (_Float16*)x16, rs, (int)H, \
+                     (int)L_all, (int)l0, (int)E)
+  if (Kt <= 2048)
+    QL_HEADS(1);
+  else if (Kt <= 4096)
+    QL_HEADS(2);
+  else if (Kt <= 8192)
+    QL_HEADS(4);
+  else
+    QL_HEADS(8);
+#undef QL_HEADS
+  return hipGetLastError();
+}
+
+hipError_t heads_to_f16_launch(int dtype, const void* o, int64_t H, int64_t L_all, int64_t l0, int64_t rows,
+                               const void* extra, int64_t E, void* x16, float* row_scale, hipStream_t stream) {
+  return dtype == kBF16 ? heads_launch_r<kBF16>(o, extra, x16, row_scale, H, L_all, l0, rows, E, stream)
+                        : heads_launch_r<kF16>(o, extra, x16, row_scale, H, L_all, l0, rows, E, stream);
 }
 
 hipError_t gated_residual_launch(int dtype, void* out, const void* x, const void* gate, const void* y, int64_t M,

@@ -112,5 +112,7 @@ hipError_t qk_norm_rope_launch(int dtype, const void* qkv, const void* q_norm, c
                                int64_t l0, float eps, hipStream_t stream);
 hipError_t gated_residual_launch(int dtype, void* out, const void* x, const void* gate, const void* y, int64_t M,
                                  int64_t K, hipStream_t stream);
+hipError_t heads_to_f16_launch(int dtype, const void* o, int64_t H, int64_t L_all, int64_t l0, int64_t rows,
+                               const void* extra, int64_t E, void* x16, float* row_scale, hipStream_t stream);
 
 }  // namespace qlinear

@@ -226,12 +226,24 @@ def _heads_into(attn: "SelfAttention", qkv: torch.Tensor, cos, sin, q, k, v, l_o
                           attn.heads, out=(q[b], k[b], v[b]), l_offset=l_offset)
 
 
-def _sdpa(q, k, v) -> torch.Tensor:
-    """SDPA on [B, H, L, D] (flash / memory-efficient kernels only) -> [B, L, H D]."""
+def _sdpa_heads(q, k, v) -> torch.Tensor:
+    """SDPA on [B, H, L, D] (flash / memory-efficient kernels only), output kept head-major."""
     from torch.nn.attention import SDPBackend, sdpa_kernel
     with sdpa_kernel([SDPBackend.FLASH_ATTENTION, SDPBackend.EFFICIENT_ATTENTION]):
-        o = F.scaled_dot_product_attention(q, k, v)
-    return o.transpose(1, 2).flatten(2)
+        return F.scaled_dot_product_attention(q, k, v).contiguous()
+
+
+def _heads_staged(o: torch.Tensor, l_offset: int, rows: int, extra: torch.Tensor | None = None) -> Staged:
+    """Rows [l_offset, l_offset + rows) of o [B, H, L, D] flattened over heads (followed by
+    extra [B, rows, E]) as the next GEMM's fp16 operand: the head transpose, the concatenation
+    and the staging pass in one kernel per batch item."""
+    B = o.shape[0]
+    parts = [_lib.heads_to_f16(o[b], l_offset, rows, extra[b] if extra is not None else None) for b in range(B)]
+    if B == 1:
+        x16, rs = parts[0]
+    else:
+        x16, rs = torch.cat([p[0] for p in parts]), torch.cat([p[1] for p in parts])
+    return Staged(x16, rs, (B, rows), o.dtype)
 
 
 class MLPEmbedder(torch.nn.Module):
@@ -315,11 +327,11 @@ class DoubleStreamBlock(torch.nn.Module):
         q, k, v = (torch.empty(B, self.heads, n_txt + n_img, D, dtype=img.dtype, device=img.device) for _ in range(3))
         _heads_into(self.txt_attn, _linear(self.txt_attn.qkv, _adaln(txt, t_sh1, t_sc1)), cos, sin, q, k, v, 0)
         _heads_into(self.img_attn, _linear(self.img_attn.qkv, _adaln(img, i_sh1, i_sc1)), cos, sin, q, k, v, n_txt)
-        o = _sdpa(q, k, v)
-        img = _residual(img, i_g1, _linear(self.img_attn.proj, o[:, n_txt:]))
+        o = _sdpa_heads(q, k, v)
+        img = _residual(img, i_g1, _linear(self.img_attn.proj, _heads_staged(o, n_txt, n_img)))
         h = _linear(self.img_mlp[0], _adaln(img, i_sh2, i_sc2), gelu=True)
         img = _residual(img, i_g2, _linear(self.img_mlp[2], h), inplace=True)
-        txt = _residual(txt, t_g1, _linear(self.txt_attn.proj, o[:, :n_txt]))
+        txt = _residual(txt, t_g1, _linear(self.txt_attn.proj, _heads_staged(o, 0, n_txt)))
         h = _linear(self.txt_mlp[0], _adaln(txt, t_sh2, t_sc2), gelu=True)
         txt = _residual(txt, t_g2, _linear(self.txt_mlp[2], h), inplace=True)
         return img, txt
@@ -355,17 +367,15 @@ class SingleStreamBlock(torch.nn.Module):
         h3 = 3 * self.hidden
         B, L, _ = x.shape
         D = self.hidden // self.heads
-        # linear2's input [attention | gelu(mlp)] assembled in one buffer
-        cat = torch.empty(B, L, self.linear2.in_features, dtype=x.dtype, device=x.device)
         q, k, v = (torch.empty(B, self.heads, L, D, dtype=x.dtype, device=x.device) for _ in range(3))
         for b in range(B):
             _lib.qk_norm_rope(_linear(self.linear1, Staged(st.x16[b * L:(b + 1) * L], st.row_scale[b * L:(b + 1) * L],
                                                            (L,), x.dtype), rows=slice(0, h3)),
                               self.norm.query_norm.scale, self.norm.key_norm.scale, cos[b, 0], sin[b, 0], self.heads,
                               out=(q[b], k[b], v[b]))
-        cat[..., h3 // 3:] = _linear(self.linear1, st, gelu=True, rows=slice(h3, None))
-        cat[..., :h3 // 3] = _sdpa(q, k, v)
-        return _residual(x, gate, _linear(self.linear2, cat))
+        mlp = _linear(self.linear1, st, gelu=True, rows=slice(h3, None))
+        # linear2's input [attention | gelu(mlp)] gathered straight into its fp16 operand
+        return _residual(x, gate, _linear(self.linear2, _heads_staged(_sdpa_heads(q, k, v), 0, L, mlp)))
 
 
 class LastLayer(torch.nn.Module):

@@ -201,6 +201,15 @@ int qlinear_qk_norm_rope(int dtype, const void* qkv, const void* q_norm, const v
                          int64_t L, int64_t H, int64_t D, int64_t L_out, int64_t l_offset,
                          float eps, void* stream);
 
+/* Attention output to the next GEMM's operand: row l of x16 [rows, H * D + E] is the head-major
+ * o[:, l_offset + l, :] ([H, L_all, D], the layout attention returns) flattened over heads,
+ * followed by extra[l, :] ([rows, E], may be NULL with E == 0), written as qlinear_rows_to_f16
+ * writes (row-scaled fp16, row_scale[l] = 2^e_l). dtype fp16/bf16 for o and extra; D == 128,
+ * E % 8 == 0, H * D + E <= 16384; o, extra, x16 16-byte aligned. */
+int qlinear_heads_to_f16(int dtype, const void* o, int64_t H, int64_t L_all, int64_t D,
+                         int64_t l_offset, int64_t rows, const void* extra, int64_t E, void* x16,
+                         float* row_scale, void* stream);
+
 /* Gated residual: out[m, k] = x[m, k] + gate[k] * y[m, k]; out may be x (in place) but must
  * not overlap it otherwise; out, x, gate, y of one dtype (fp32/fp16/bf16), K % 8 == 0, 16-byte
  * aligned. */

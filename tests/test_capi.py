@@ -173,6 +173,15 @@ def test_fused_dit_entry_points_check_arguments(lib):
     assert qk(2, None, None, None, None, None, None, None, None, 4, 2, 128, 6, 2, 1e-6, None) == QL_ERR_ARG
     assert qk(2, p16, p16, p16, p16, p16, p16, p16, ctypes.c_void_p(258), 4, 2, 128, 6, 2, 1e-6,
               None) == QL_ERR_ALIGN
+    hd = lib.qlinear_heads_to_f16
+    assert hd(0, None, 2, 8, 128, 0, 8, None, 0, None, None, None) == QL_ERR_DTYPE
+    assert hd(2, None, 2, 8, 64, 0, 8, None, 0, None, None, None) == QL_ERR_SHAPE
+    assert hd(2, None, 2, 8, 128, 4, 5, None, 0, None, None, None) == QL_ERR_SHAPE  # rows past L
+    assert hd(2, None, 2, 8, 128, 0, 8, None, 12, None, None, None) == QL_ERR_SHAPE  # E % 8
+    assert hd(2, None, 24, 8, 128, 0, 8, None, 16384, None, None, None) == QL_ERR_SHAPE  # row too long
+    assert hd(2, None, 2, 8, 128, 0, 0, None, 0, None, None, None) == QL_OK
+    assert hd(2, p16, 2, 8, 128, 0, 8, None, 8, p16, p16, None) == QL_ERR_ARG  # E > 0 needs extra
+    assert hd(2, p16, 2, 8, 128, 0, 8, ctypes.c_void_p(264), 8, p16, p16, None) == QL_ERR_ALIGN
     res = lib.qlinear_gated_residual
     assert res(3, None, None, None, None, 4, 64, None) == QL_ERR_DTYPE
     assert res(2, None, None, None, None, 4, 12, None) == QL_ERR_SHAPE

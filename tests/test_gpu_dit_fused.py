@@ -111,3 +111,27 @@ def test_engine_blocks_leave_inputs_unchanged():
         m.single_blocks[0](x, vec, cos, sin)
         torch.cuda.synchronize()
     assert torch.equal(img, i0) and torch.equal(txt, t0) and torch.equal(x, x0)
+
+
+@pytest.mark.parametrize("H,L,l0,rows,E", [(1, 5, 0, 5, 0), (24, 300, 40, 260, 0), (2, 64, 0, 64, 512),
+                                           (24, 130, 0, 130, 12288)])
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_heads_to_f16(H, L, l0, rows, E, dt):
+    """Head-major attention rows (+ a second source) into the row-scaled fp16 GEMM operand: the
+    values are the exact inputs (16-bit values scale into fp16 without rounding unless they fall
+    below the row's range), the layout is [heads | extra]."""
+    print(f"heads_to_f16 H={H} L={L} l0={l0} rows={rows} E={E} {dt}", flush=True)
+    g = torch.Generator().manual_seed(H + L + E)
+    o = torch.randn(H, L, 128, generator=g).to(dt)
+    extra = (torch.randn(rows, E, generator=g) * 5).to(dt) if E else None
+    x16, rs = _lib.heads_to_f16(o.cuda(), l0, rows, extra.cuda() if extra is not None else None)
+    torch.cuda.synchronize()
+    ref = o[:, l0:l0 + rows].transpose(0, 1).reshape(rows, H * 128).double()
+    if E:
+        ref = torch.cat([ref, extra.double()], 1)
+    y = x16.cpu().double() * rs.cpu().double()[:, None]
+    amax = x16.cpu().double().abs().amax(-1)
+    assert torch.all((amax >= 2.0 ** 14) & (amax <= 2.0 ** 15))
+    rowmax = ref.abs().amax(-1, keepdim=True)
+    assert torch.all((y - ref).abs() <= 2.0 ** -11 * ref.abs() + 2.0 ** -24 * rs.cpu().double()[:, None])
+    assert torch.all(rowmax > 0)
