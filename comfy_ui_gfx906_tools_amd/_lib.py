@@ -61,6 +61,9 @@ SIGNATURES = {
     "qlinear_rotate_rows_to_f16": (_c_int, [_c_int, _c_vp, _c_vp, _c_int, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
     "qlinear_heads_to_f16": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp,
                                       _c_vp, _c_vp]),
+    "qlinear_quantize_int8_block32": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
+    "qlinear_gemm_int8_block32": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64,
+                                           _c_vp]),
     "qlinear_gated_residual": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
 }
 
@@ -315,6 +318,59 @@ def w8a8_gemm(xq: torch.Tensor, x_scale: torch.Tensor, wq: torch.Tensor, w_scale
                                    bias.data_ptr() if bias is not None else None, y.data_ptr(), M, N, K,
                                    _stream_ptr(xq.device))
     _check(rc, "w8a8_gemm")
+    return y
+
+
+def quantize_int8_block32(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Block-32 int8 quantize of x [M, K] -> (int8 [M, K], fp32 [M, K/32])."""
+    lib = load_library()
+    x = _dev_tensor(x, "x")
+    if x.dim() != 2 or x.shape[1] % 32 != 0 or x.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        raise RuntimeError(f"x must be a float32/float16/bfloat16 [M, K] tensor with K % 32 == 0, got {x.dtype} "
+                           f"{list(x.shape)}")
+    M, K = x.shape
+    q = torch.empty((M, K), dtype=torch.int8, device=x.device)
+    s = torch.empty((M, K // 32), dtype=torch.float32, device=x.device)
+    if M == 0:
+        return q, s
+    with torch.cuda.device(x.device):
+        rc = lib.qlinear_quantize_int8_block32(_DTYPE_CODE[x.dtype], x.data_ptr(), q.data_ptr(), s.data_ptr(), M, K,
+                                               _stream_ptr(x.device))
+    _check(rc, "quantize_int8_block32")
+    return q, s
+
+
+def gemm_int8_block32(a: torch.Tensor, a_scale: torch.Tensor, b: torch.Tensor, b_scale: torch.Tensor,
+                      bias: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float32) -> torch.Tensor:
+    """[M, N] = block-32 int8 A [M, K] x B [N, K]^T with the reference's per-block fmaf order."""
+    lib = load_library()
+    a, b = _dev_tensor(a, "A"), _dev_tensor(b, "B")
+    if a.device != b.device:
+        raise RuntimeError("A and B must be on the same device")
+    if a.dtype != torch.int8 or b.dtype != torch.int8:
+        raise RuntimeError("A and B must be int8")
+    if a.dim() != 2 or b.dim() != 2 or a.shape[1] != b.shape[1] or a.shape[1] % 32 != 0:
+        raise RuntimeError(f"expected A [M, K], B [N, K], K % 32 == 0; got A {list(a.shape)} B {list(b.shape)}")
+    M, N, K = a.shape[0], b.shape[0], a.shape[1]
+    a_scale, b_scale = _dev_tensor(a_scale, "A_scale"), _dev_tensor(b_scale, "B_scale")
+    if a_scale.dtype != torch.float32 or b_scale.dtype != torch.float32:
+        raise RuntimeError("scales must be float32")
+    if a_scale.numel() != M * (K // 32) or b_scale.numel() != N * (K // 32):
+        raise RuntimeError(f"scales must be [M, K/32] / [N, K/32], got {list(a_scale.shape)} / {list(b_scale.shape)}")
+    if out_dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        raise RuntimeError(f"unsupported dtype {out_dtype}, expected float32/float16/bfloat16")
+    if bias is not None:
+        bias = _dev_tensor(bias, "bias")
+        if bias.dtype != out_dtype or bias.numel() != N:
+            raise RuntimeError(f"bias must be {out_dtype} [{N}], got {bias.dtype} {list(bias.shape)}")
+    y = torch.empty((M, N), dtype=out_dtype, device=a.device)
+    if M == 0:
+        return y
+    with torch.cuda.device(a.device):
+        rc = lib.qlinear_gemm_int8_block32(_DTYPE_CODE[out_dtype], a.data_ptr(), a_scale.data_ptr(), b.data_ptr(),
+                                           b_scale.data_ptr(), bias.data_ptr() if bias is not None else None,
+                                           y.data_ptr(), M, N, K, _stream_ptr(a.device))
+    _check(rc, "gemm_int8_block32")
     return y
 
 

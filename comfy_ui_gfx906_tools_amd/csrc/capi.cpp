@@ -565,4 +565,53 @@ int qlinear_heads_to_f16(int dtype, const void* o, int64_t H, int64_t L_all, int
   return ok();
 }
 
+int qlinear_quantize_int8_block32(int x_dtype, const void* x, int8_t* q, float* scale, int64_t rows, int64_t K,
+                                  void* stream) {
+  if (x_dtype != QL_F32 && x_dtype != QL_F16 && x_dtype != QL_BF16)
+    return fail(QL_ERR_DTYPE, "unsupported dtype %s (%d), expected float32/float16/bfloat16", dtype_name(x_dtype),
+                x_dtype);
+  if (rows < 0 || K < 32 || K % 32 != 0 || rows * (K / 32) > ((int64_t)1 << 40))
+    return fail(QL_ERR_SHAPE, "x must be [rows, K] with K %% 32 == 0, got [%lld, %lld]", (long long)rows, (long long)K);
+  if (rows == 0) return ok();
+  if (!x || !q || !scale) return fail(QL_ERR_ARG, "null x / q / scale pointer");
+  if (!aligned16(x) || !aligned16(q) || ((uintptr_t)scale & 3u))
+    return fail(QL_ERR_ALIGN, "x and q must be 16-byte aligned, scale 4-byte aligned");
+  const hipError_t e = quantize_int8_block32_launch(x_dtype, x, q, scale, rows * (K / 32), (hipStream_t)stream);
+  if (e != hipSuccess) return fail(QL_ERR_LAUNCH, "quantize_int8_block32 launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int qlinear_gemm_int8_block32(int out_dtype, const int8_t* a, const float* a_scale, const int8_t* b, const float* b_scale,
+                              const void* bias, void* y, int64_t M, int64_t N, int64_t K, void* stream) {
+  if (out_dtype != QL_F32 && out_dtype != QL_F16 && out_dtype != QL_BF16)
+    return fail(QL_ERR_DTYPE, "out dtype %s (%d) unsupported, expected float32/float16/bfloat16", dtype_name(out_dtype),
+                out_dtype);
+  if (M < 0 || N <= 0 || K < 32 || K % 32 != 0 || M > INT32_MAX / 2 || N > INT32_MAX / 2 || K > (1 << 30))
+    return fail(QL_ERR_SHAPE, "expected A [M, K], B [N, K] with K %% 32 == 0, K >= 32, N > 0; got M=%lld N=%lld K=%lld",
+                (long long)M, (long long)N, (long long)K);
+  const int64_t tiles = ((M + 127) / 128) * ((N + 127) / 128);
+  if (tiles > INT32_MAX) return fail(QL_ERR_SHAPE, "too many 128 x 128 tiles (M=%lld N=%lld)", (long long)M, (long long)N);
+  if (M == 0) return ok();
+  if (!a || !a_scale || !b || !b_scale || !y) return fail(QL_ERR_ARG, "null a / a_scale / b / b_scale / y pointer");
+  if (!aligned16(a) || !aligned16(b)) return fail(QL_ERR_ALIGN, "a and b must be 16-byte aligned");
+  if (((uintptr_t)a_scale & 3u) || ((uintptr_t)b_scale & 3u))
+    return fail(QL_ERR_ALIGN, "a_scale and b_scale must be 4-byte aligned");
+  W4A4Params p{};
+  p.a = a;
+  p.as = a_scale;
+  p.b = b;
+  p.bs = b_scale;
+  p.bias = bias;
+  p.y = y;
+  p.M = (int)M;
+  p.N = (int)N;
+  p.K = (int)K;
+  p.out_dtype = out_dtype;
+  p.tiles_m = (int)((M + 127) / 128);
+  p.tiles_n = (int)((N + 127) / 128);
+  const hipError_t e = int8_block32_launch(p, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(QL_ERR_LAUNCH, "gemm_int8_block32 launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
 }  // extern "C"

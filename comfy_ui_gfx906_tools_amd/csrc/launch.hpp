@@ -97,6 +97,10 @@ struct W4A4Params {
   int tiles_m, tiles_n;  // 128 x 128 tiles
 };
 hipError_t w4a4_launch(int qblock, const W4A4Params& p, hipStream_t stream);
+// The same kernel with int8 codes ([M, K] / [N, K], block-32 scales): the reference's gemm_int8.
+hipError_t int8_block32_launch(const W4A4Params& p, hipStream_t stream);
+hipError_t quantize_int8_block32_launch(int dtype, const void* x, int8_t* q, float* scale, int64_t blocks,
+                                       hipStream_t stream);
 
 // Activation rotation + fp16 staging in one pass (rotate.hip): group 32 / 64 / 128, K % group == 0,
 // K <= 16384.

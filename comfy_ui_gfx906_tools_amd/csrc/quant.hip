@@ -194,6 +194,59 @@ __global__ __launch_bounds__(kQThreads) void repack_q4_0_kernel(const uint16_t* 
   scale[b] = f16_bits_to_f32(src[0]);
 }
 
+// Block-32 int8 quantize, the reference's quantize_int8_kernel rule (csrc/int8_gemm.hip:215-246):
+// one thread per 32-element block, s = max(amax, 1e-8) * (1/127), q = clamp(rint(v / s), -127, 127),
+// the block read with 16-byte loads and its 32 codes written as two 16-byte stores.
+template <int DT>
+__global__ __launch_bounds__(kQThreads) void quantize_int8_block32_kernel(const void* __restrict__ x,
+                                                                          int8_t* __restrict__ q,
+                                                                          float* __restrict__ scale, long blocks) {
+  const long b = (long)blockIdx.x * kQThreads + threadIdx.x;
+  if (b >= blocks) return;
+  const size_t base = (size_t)b * 32;
+  float v[32];
+  if constexpr (DT == kF32) {
+#pragma unroll
+    for (int c = 0; c < 8; ++c) {
+      const u32x4 w = *(const u32x4*)((const float*)x + base + 4 * c);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t bits = w[e];
+        v[4 * c + e] = __builtin_bit_cast(float, bits);
+      }
+    }
+  } else {
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const u32x4 w = *(const u32x4*)((const uint16_t*)x + base + 8 * c);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const uint32_t lo = w[e] & 0xFFFFu, hi = w[e] >> 16;
+        v[8 * c + 2 * e] = DT == kBF16 ? bf16_bits_to_f32(lo) : f16_bits_to_f32(lo);
+        v[8 * c + 2 * e + 1] = DT == kBF16 ? bf16_bits_to_f32(hi) : f16_bits_to_f32(hi);
+      }
+    }
+  }
+  float amax = 0.0f;
+#pragma unroll
+  for (int e = 0; e < 32; ++e) amax = fmaxf(amax, fabsf(v[e]));
+  const float s = __fmul_rn(fmaxf(amax, 1e-8f), 1.0f / 127.0f);
+  u32x4 out[2];
+#pragma unroll
+  for (int w = 0; w < 8; ++w) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int c = (int)fminf(fmaxf(rintf(__fdiv_rn(v[4 * w + e], s)), -127.0f), 127.0f);
+      word |= (uint32_t)(c & 0xFF) << (8 * e);
+    }
+    out[w >> 2][w & 3] = word;
+  }
+  *(u32x4*)(q + base) = out[0];
+  *(u32x4*)(q + base + 16) = out[1];
+  scale[b] = s;
+}
+
 }  // namespace
 
 hipError_t repack_q4_0_launch(const void* raw, void* packed, float* scale, int64_t blocks, hipStream_t stream) {
@@ -252,6 +305,24 @@ hipError_t quantize_int8_per_token_launch(int dtype, const void* x, int8_t* q, f
       break;
     default:
       hipLaunchKernelGGL(quantize_int8_row_kernel<kBF16>, grid, dim3(kQThreads), 0, stream, x, q, scale, (int)K);
+      break;
+  }
+  return hipGetLastError();
+}
+
+hipError_t quantize_int8_block32_launch(int dtype, const void* x, int8_t* q, float* scale, int64_t blocks,
+                                       hipStream_t stream) {
+  const dim3 grid((unsigned)((blocks + kQThreads - 1) / kQThreads));
+  switch (dtype) {
+    case kF32:
+      hipLaunchKernelGGL(quantize_int8_block32_kernel<kF32>, grid, dim3(kQThreads), 0, stream, x, q, scale, (long)blocks);
+      break;
+    case kF16:
+      hipLaunchKernelGGL(quantize_int8_block32_kernel<kF16>, grid, dim3(kQThreads), 0, stream, x, q, scale, (long)blocks);
+      break;
+    default:
+      hipLaunchKernelGGL(quantize_int8_block32_kernel<kBF16>, grid, dim3(kQThreads), 0, stream, x, q, scale,
+                         (long)blocks);
       break;
   }
   return hipGetLastError();

@@ -1,4 +1,4 @@
-// W4A4 GEMM on gfx950 with the reference's production numerics (nodes/ComfyUI-Gfx906Int4/csrc/
+// Block-scaled int4 (W4A4) and int8 GEMMs on gfx950 with the reference's numerics (nodes/ComfyUI-Gfx906Int4/csrc/
 // int4_gemm_scaled.hip:53-191, gemm_int4 with splits = 1): A [M, K/2] and B [N, K/2] packed int4
 // (two's-complement nibbles, low nibble first), scales As [M, K/qb], Bs [N, K/qb] fp32, qb = 32 or
 // 16. For every quant block in K order: ip = exact int32 dot of the block's codes, then
@@ -11,13 +11,16 @@
 //   MFMA returns 256 * ip exactly (|256 ip| <= 2^19), and the A scales are taken as as * 2^-8
 //   (exact), so fmaf(float(256 ip), (as * 2^-8) * bs, acc) rounds exactly like the reference's
 //   fmaf(float(ip), as * bs, acc) (the two products are the same real number).
+// * int8 (block-32 gemm_int8, csrc/int8_gemm.hip:66-213 of the reference, same per-block fmaf order):
+//   the codes go to the MFMA as they are (partial = ip), scales unscaled.
 // * 128 x 128 tile per 256-thread workgroup, 4 waves as 2 x 2, each 64 x 64 = 4 x 4 fragments.
-//   A stage is 4 quant blocks (64 B of codes per row): global -> registers -> LDS, double
+//   A stage is 64 B of codes per row (4 int4 blocks or 2 int8 blocks): global -> registers -> LDS, double
 //   buffered, one barrier per stage. In LDS a row keeps, per lane group j, the 4 dwords (one per
 //   block) that lane group j feeds to the MFMA, so a lane reads its operands for the whole stage
 //   with one 16-byte read; scales are stored block-major so a lane's 4 rows are one 16-byte read.
-// * Lane (r, j) of a fragment supplies row r and K slots 8j .. 8j+7 of the block, i.e. dword j of
-//   the row's 16-byte block (A and B use the same slot order, so the dot is unchanged); the
+// * Lane (r, j) of a fragment supplies row r and K slots 8j .. 8j+7 of the block: int4, dword j of
+//   the row's 16-byte block (even K in the low dword, odd K in the high one -- A and B use the same
+//   slot order, so the dot is unchanged); int8, bytes 8j .. 8j+7 of the 32-byte block. The
 //   accumulator lane layout is (row 4j + e, column r).
 #include "common.hpp"
 #include "launch.hpp"
@@ -27,8 +30,7 @@ namespace qlinear {
 namespace {
 
 constexpr int kW4BM = 128, kW4BN = 128;
-constexpr int kW4StageBlocks = 4;                   // quant blocks of 32 K per stage
-constexpr int kW4RowBytes = kW4StageBlocks * 16;    // packed bytes per row per stage
+constexpr int kW4RowBytes = 64;  // code bytes per row per stage (4 int4 blocks or 2 int8 blocks)
 constexpr int kW4GroupM = 8;
 
 // 8 codes of a dword (K = 2t in the low nibble of byte t, 2t + 1 in the high one) as 8 int8 lanes
@@ -39,8 +41,11 @@ __device__ __forceinline__ long unpack_x16(uint32_t w) {
   return (long)(((uint64_t)odd << 32) | even);
 }
 
-template <int SUB>
+template <int SUB, bool kI8>
 __global__ __launch_bounds__(256) void w4a4_gemm_kernel(W4A4Params p) {
+  constexpr int kBlkBytes = kI8 ? 32 : 16;               // code bytes per quant block of 32 K
+  constexpr int kW4StageBlocks = kW4RowBytes / kBlkBytes;
+  constexpr int kChunksPerBlk = kBlkBytes / 16;
   constexpr int kScaleCols = SUB * kW4StageBlocks;  // scale columns per stage
   __shared__ __attribute__((aligned(16))) uint8_t lds_a[2][kW4BM * kW4RowBytes];
   __shared__ __attribute__((aligned(16))) uint8_t lds_b[2][kW4BN * kW4RowBytes];
@@ -62,7 +67,7 @@ __global__ __launch_bounds__(256) void w4a4_gemm_kernel(W4A4Params p) {
   const int m0 = tm * kW4BM, n0 = tn * kW4BN;
   const uint8_t* A = (const uint8_t*)p.a;
   const uint8_t* B = (const uint8_t*)p.b;
-  const size_t row_bytes = (size_t)K / 2;
+  const size_t row_bytes = (size_t)K * kBlkBytes / 32;
 
   // ---- stage loads: 512 16-byte chunks of A and of B (row c / 4, block c % 4), 128 x kScaleCols
   //      scales of each ------------------------------------------------------------------------
@@ -71,12 +76,12 @@ __global__ __launch_bounds__(256) void w4a4_gemm_kernel(W4A4Params p) {
   auto load_regs = [&](int s) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const int c = tid + 256 * i, r = c >> 2, kb = s * kW4StageBlocks + (c & 3);
+      const int c = tid + 256 * i, r = c >> 2;
+      const int kb = s * kW4StageBlocks + (c & 3) / kChunksPerBlk, part = (c & 3) % kChunksPerBlk;
       const bool ka = kb < KB;
-      ra[i] = (ka && m0 + r < M) ? *(const u32x4*)(A + (size_t)(m0 + r) * row_bytes + (size_t)kb * 16)
-                                 : u32x4{0u, 0u, 0u, 0u};
-      rb[i] = (ka && n0 + r < N) ? *(const u32x4*)(B + (size_t)(n0 + r) * row_bytes + (size_t)kb * 16)
-                                 : u32x4{0u, 0u, 0u, 0u};
+      const size_t off = (size_t)kb * kBlkBytes + 16 * part;
+      ra[i] = (ka && m0 + r < M) ? *(const u32x4*)(A + (size_t)(m0 + r) * row_bytes + off) : u32x4{0u, 0u, 0u, 0u};
+      rb[i] = (ka && n0 + r < N) ? *(const u32x4*)(B + (size_t)(n0 + r) * row_bytes + off) : u32x4{0u, 0u, 0u, 0u};
     }
     // threads 0-127: A scales of row tid (taken as as * 2^-8); 128-255: B scales of row tid - 128
     const int r = tid & 127;
@@ -88,16 +93,20 @@ __global__ __launch_bounds__(256) void w4a4_gemm_kernel(W4A4Params p) {
     for (int q = 0; q < kScaleCols; ++q) {
       const int col = s * kScaleCols + q;
       const float v = (rok && col < SC) ? sp[(size_t)gr * SC + col] : 0.0f;
-      rsa[q] = is_a ? v * 0.00390625f : v;
+      rsa[q] = (is_a && !kI8) ? v * 0.00390625f : v;
     }
   };
   auto store_lds = [&](int buf) {
 #pragma unroll
     for (int i = 0; i < 2; ++i) {
-      const int c = tid + 256 * i, r = c >> 2, b = c & 3;
+      const int c = tid + 256 * i, r = c >> 2, q = c & 3;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const int off = r * kW4RowBytes + ((j ^ (r & 3)) << 4) + 4 * b;
+        // int4: chunk q = block q, dword j -> lane group j, slot q; int8: chunk q = half q % 2 of block
+        // q / 2, dword j -> lane group 2 (q % 2) + j / 2, slot 2 (q / 2) + j % 2
+        const int grp = kI8 ? 2 * (q & 1) + (j >> 1) : j;
+        const int slot = kI8 ? 2 * (q >> 1) + (j & 1) : q;
+        const int off = r * kW4RowBytes + ((grp ^ (r & 3)) << 4) + 4 * slot;
         *(uint32_t*)(lds_a[buf] + off) = ra[i][j];
         *(uint32_t*)(lds_b[buf] + off) = rb[i][j];
       }
@@ -131,15 +140,21 @@ __global__ __launch_bounds__(256) void w4a4_gemm_kernel(W4A4Params p) {
 #pragma unroll
     for (int b = 0; b < kW4StageBlocks; ++b) {
       if (b >= nb) break;
+      auto operand = [&](const u32x4& raw) -> long {
+        if constexpr (kI8)
+          return (long)(((uint64_t)raw[2 * b + 1] << 32) | raw[2 * b]);
+        else
+          return unpack_x16(raw[b]);
+      };
       long bop[4];
 #pragma unroll
-      for (int fn = 0; fn < 4; ++fn) bop[fn] = unpack_x16(b_raw[fn][b]);
+      for (int fn = 0; fn < 4; ++fn) bop[fn] = operand(b_raw[fn]);
 #pragma unroll
       for (int sub = 0; sub < SUB; ++sub) {
         long aop[4];
 #pragma unroll
         for (int fm = 0; fm < 4; ++fm) {
-          const long v = unpack_x16(a_raw[fm][b]);
+          const long v = operand(a_raw[fm]);
           aop[fm] = (SUB == 1 || (j4 >> 1) == sub) ? v : 0l;  // qb = 16: K slots of this half only
         }
         i32x4 part[4][4];
@@ -192,9 +207,15 @@ __global__ __launch_bounds__(256) void w4a4_gemm_kernel(W4A4Params p) {
 hipError_t w4a4_launch(int qblock, const W4A4Params& p, hipStream_t stream) {
   const dim3 grid((unsigned)(p.tiles_m * p.tiles_n)), block(256);
   if (qblock == 32)
-    hipLaunchKernelGGL(w4a4_gemm_kernel<1>, grid, block, 0, stream, p);
+    hipLaunchKernelGGL((w4a4_gemm_kernel<1, false>), grid, block, 0, stream, p);
   else
-    hipLaunchKernelGGL(w4a4_gemm_kernel<2>, grid, block, 0, stream, p);
+    hipLaunchKernelGGL((w4a4_gemm_kernel<2, false>), grid, block, 0, stream, p);
+  return hipGetLastError();
+}
+
+hipError_t int8_block32_launch(const W4A4Params& p, hipStream_t stream) {
+  const dim3 grid((unsigned)(p.tiles_m * p.tiles_n)), block(256);
+  hipLaunchKernelGGL((w4a4_gemm_kernel<1, true>), grid, block, 0, stream, p);
   return hipGetLastError();
 }
 

@@ -45,3 +45,39 @@ def gemm_int4(A_packed: torch.Tensor, A_scale: torch.Tensor, B_packed: torch.Ten
 def gemm_int4_auto_splits(M: int, N: int, K: int) -> int:
     """Split-K count gemm_int4 uses for [M, K] x [N, K]^T: always 1 here (no K cut)."""
     return 1
+
+
+def quantize_int8(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """x [M, K] float32/16/bf16 on the GPU, K % 32 == 0 -> (int8 [M, K], scale fp32 [M, K/32])."""
+    if not (isinstance(x, torch.Tensor) and x.is_cuda):
+        raise RuntimeError("x must be on device")
+    if x.dim() != 2 or x.shape[1] % 32 != 0:
+        raise RuntimeError(f"x must be [M, K] with K % 32 == 0, got {list(x.shape)}")
+    return _lib.quantize_int8_block32(x)
+
+
+def gemm_int8(A: torch.Tensor, A_scale: torch.Tensor, B: torch.Tensor, B_scale: torch.Tensor,
+              bias: torch.Tensor | None, out_dtype: torch.dtype, config: int = 0) -> torch.Tensor:
+    """[M, N] in out_dtype = block-32 int8 A [M, K] x B [N, K]^T (+ bias in out_dtype)."""
+    if not (A.is_cuda and B.is_cuda):
+        raise RuntimeError("inputs must be on device")
+    if not 0 <= int(config) <= 3:
+        raise RuntimeError(f"config must be in [0, 3], got {config}")
+    return _lib.gemm_int8_block32(A, A_scale, B, B_scale, bias, out_dtype=out_dtype)
+
+
+def w4a16_linear(x: torch.Tensor, w_q4: torch.Tensor, w_scale: torch.Tensor, bias: torch.Tensor | None = None,
+                 out_dtype: torch.dtype | None = None) -> torch.Tensor:
+    """x [M, K] @ dequant(w_q4, w_scale)^T (+ bias) on the W4A16 engine."""
+    return _lib.w4a16_gemm(x, w_q4, w_scale, bias, out_dtype=out_dtype)
+
+
+def quantize_int8_per_token(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """x [M, K] -> (int8 [M, K], fp32 [M]): the int8 rule with one block per row."""
+    return _lib.quantize_int8_per_token(x)
+
+
+def w8a8_linear(xq: torch.Tensor, s_x: torch.Tensor, wq: torch.Tensor, s_w: torch.Tensor,
+                bias: torch.Tensor | None = None, out_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """float(xq @ wq^T in int32) * (s_x[m] * s_w[n]) (+ bias) in out_dtype."""
+    return _lib.w8a8_gemm(xq, s_x, wq, s_w, bias, out_dtype=out_dtype)

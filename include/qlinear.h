@@ -175,6 +175,23 @@ int qlinear_w4a4_gemm(int out_dtype, const void* a_q4, const float* a_scale, con
                       int64_t K, int qblock, void* stream);
 
 /* ---------------------------------------------------------------------------------------
+ * Block-32 int8, the reference's gemm_int8 / quantize_int8 (csrc/int8_gemm.hip:66-252,
+ * gemm_int8_dispatch / quantize_int8_dispatch :280-295; ext.quantize_int8 / ext.gemm_int8,
+ * csrc/binding.cpp:173-217):
+ *   quantize: per 32 elements s = max(amax, 1e-8) * (1/127), q = clamp(rint(x / s), -127, 127)
+ *             -> q int8 [rows, K], scale fp32 [rows, K/32]
+ *   gemm:     per block in K order ip = exact int32 dot, acc = fmaf(float(ip), as * bs, acc);
+ *             y = acc (+ bias, dtype out_dtype) rounded to out_dtype. Bit-identical to the
+ *             reference's kernel (any of its tile configs: they share this order).
+ * K % 32 == 0; x / q / a / b 16-byte aligned.
+ * ------------------------------------------------------------------------------------- */
+int qlinear_quantize_int8_block32(int x_dtype, const void* x, int8_t* q, float* scale, int64_t rows,
+                                  int64_t K, void* stream);
+int qlinear_gemm_int8_block32(int out_dtype, const int8_t* a, const float* a_scale, const int8_t* b,
+                              const float* b_scale, const void* bias, void* y, int64_t M, int64_t N,
+                              int64_t K, void* stream);
+
+/* ---------------------------------------------------------------------------------------
  * Fused DiT block glue. No counterpart in the reference: its node patches only the Linears of
  * ComfyUI's Flux model (nodes/ComfyUI-Gfx906Int4/nodes.py:71-124, 447-599) and the layer norms,
  * modulation, QK-norm, RoPE and gated residuals run as separate torch ops around them. Each entry

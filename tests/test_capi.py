@@ -151,6 +151,21 @@ def test_w4a4_entry_point_checks_arguments(lib):
     assert f(0, p16, ctypes.c_void_p(258), p16, p16, None, p16, 4, 64, 64, 16, None) == QL_ERR_ALIGN
 
 
+def test_int8_block32_entry_points_check_arguments(lib):
+    p16 = ctypes.c_void_p(256)
+    qz, gm = lib.qlinear_quantize_int8_block32, lib.qlinear_gemm_int8_block32
+    assert qz(3, None, None, None, 4, 64, None) == QL_ERR_DTYPE
+    assert qz(2, None, None, None, 4, 48, None) == QL_ERR_SHAPE
+    assert qz(2, None, None, None, 0, 64, None) == QL_OK
+    assert qz(2, None, None, None, 4, 64, None) == QL_ERR_ARG
+    assert qz(2, ctypes.c_void_p(264), p16, p16, 4, 64, None) == QL_ERR_ALIGN
+    assert gm(3, None, None, None, None, None, None, 4, 64, 64, None) == QL_ERR_DTYPE
+    assert gm(0, None, None, None, None, None, None, 4, 64, 40, None) == QL_ERR_SHAPE
+    assert gm(0, None, None, None, None, None, None, 0, 64, 64, None) == QL_OK
+    assert gm(0, None, None, None, None, None, None, 4, 64, 64, None) == QL_ERR_ARG
+    assert gm(0, p16, p16, ctypes.c_void_p(264), p16, None, p16, 4, 64, 64, None) == QL_ERR_ALIGN
+
+
 def test_fused_dit_entry_points_check_arguments(lib):
     """The fused DiT glue entry points reject bad arguments before any launch."""
     p16 = ctypes.c_void_p(256)

@@ -89,3 +89,43 @@ def test_ext_surface_errors():
     with pytest.raises(RuntimeError, match="scales must be"):
         ext.gemm_int4(a, torch.ones(4, 2, device=DEV), a, s, None, torch.float32)
     assert ext.gemm_int4_auto_splits(4608, 3072, 3072) == 1
+
+
+@pytest.mark.parametrize("M,K", [(1, 32), (7, 96), (300, 3072)])
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16, torch.float32])
+def test_quantize_int8_block32_bit_exact(M, K, dt):
+    x = (torch.randn(M, K, generator=torch.Generator().manual_seed(M + K)) * 4).to(dt)
+    x[0, :32] = 0.0
+    q, s = ext.quantize_int8(x.to(DEV))
+    q_ref, s_ref = orc.quantize_int8_rows(x.float().numpy(), block=32)
+    assert np.array_equal(q.cpu().numpy(), q_ref) and np.array_equal(s.cpu().numpy(), s_ref)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 64, 32), (37, 100, 96), (130, 257, 640), (300, 520, 1056)])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+def test_gemm_int8_block32_bit_exact(M, N, K, out_dtype):
+    """The reference's gemm_int8 (block-32 scales both sides, per-block fmaf in K order, + bias)."""
+    print(f"gemm_int8 M={M} N={N} K={K} {out_dtype}", flush=True)
+    g = np.random.default_rng(M + N + K)
+    a = g.integers(-127, 128, (M, K)).astype(np.int8)
+    b = g.integers(-127, 128, (N, K)).astype(np.int8)
+    sa = (2.0 ** g.uniform(-14, -4, (M, K // 32))).astype(np.float32)
+    sb = (2.0 ** g.uniform(-14, -4, (N, K // 32))).astype(np.float32)
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(3)).to(out_dtype)
+    y = ext.gemm_int8(*(torch.from_numpy(t).to(DEV) for t in (a, sa, b, sb)), bias.to(DEV), out_dtype)
+    ref = torch.from_numpy(orc.gemm_int8_block32(a, sa, b, sb, bias.float().numpy(), 32)).to(out_dtype)
+    assert torch.equal(y.cpu(), ref)
+
+
+def test_reference_int8_linear_pipeline_bit_exact():
+    """quantize_int8 of x and W, then gemm_int8: the reference's int8 linear, bit-exact."""
+    M, N, K = 200, 300, 1024
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(M, K, generator=g).to(torch.bfloat16)
+    w = torch.randn(N, K, generator=g) * 0.02
+    qa, sa = ext.quantize_int8(x.to(DEV))
+    qb, sb = ext.quantize_int8(w.to(DEV))
+    y = ext.gemm_int8(qa, sa, qb, sb, None, torch.float32)
+    a_ref, sa_ref = orc.quantize_int8_rows(x.float().numpy(), block=32)
+    b_ref, sb_ref = orc.quantize_int8_rows(w.numpy(), block=32)
+    assert np.array_equal(y.cpu().numpy(), orc.gemm_int8_block32(a_ref, sa_ref, b_ref, sb_ref, None, 32))
