@@ -5,10 +5,10 @@
 // at full bandwidth with as little VALU work per weight as possible; no MFMA (a 16-row MFMA tile
 // would be at most a quarter full).
 //
-// * About two waves per SIMD, each looping over its output columns n = w, w + W, w + 2W, ...
+// * About four waves per SIMD, each looping over its output columns n = w, w + W, w + 2W, ...
 //   (W = waves in the grid). Lane i takes the quant groups g = i, i + 64, ... (kR of them) of
 //   a column: 16 contiguous bytes (32 nibbles) each, so one load instruction reads 1 KiB of one
-//   weight row. The weights and scales of the next kD columns (kD = 12 / kR) are in flight by
+//   weight row. The weights and scales of the next kD columns (kD = max(2, 6 / kR)) are in flight by
 //   DMA into a wave-private LDS ring while a column is computed: enough bytes in flight for HBM
 //   latency, and memory and arithmetic overlap within every wave.
 // * Dequant without conversion instructions: with u = nibble ^ 8 = code + 8 in [0, 15], the
@@ -38,6 +38,13 @@ namespace qlinear {
 namespace {
 
 constexpr int kGvWaves = 4;  // waves per workgroup (independent)
+// Four waves per SIMD, each with 6 / kR (at least 2) columns in flight: against two waves with
+// 12 / kR columns (the same bytes in flight per CU), each wave owns half the columns, so less of
+// its arithmetic trails the last load (measured at M = 1: K = 4096, N = 10240 9.24 -> 8.95 us;
+// 3072 -> 18432 11.7 -> 10.9 us; with a single column in flight at K = 8192 it lost, 7.7 -> 8.1 us).
+// LDS: 4 waves x kD x kR x 1.25 KiB per workgroup, at most 40 KiB, so four workgroups fit a CU.
+constexpr int kGvDepth = 6;
+constexpr int kGvWavesPerSimd = 4;
 
 template <bool kBf16>
 __device__ __forceinline__ float dot2(uint32_t a, uint32_t b, float c) {
@@ -93,7 +100,7 @@ __global__ __launch_bounds__(64 * kGvWaves) void w4a16_gemv_kernel(W4A16Params p
   // and groups past K read zeros (a zero scale then zeroes the group). Every call issues exactly
   // 2 kR loads.
   constexpr int kColBytes = kR * (1024 + 256);
-  constexpr int kD = 12 / kR;  // columns in flight per wave: 15 KiB of LDS per wave
+  constexpr int kD = kGvDepth / kR >= 2 ? kGvDepth / kR : 2;  // columns in flight per wave
   __shared__ __attribute__((aligned(1024))) uint8_t lds[kGvWaves * kD * kColBytes];
   uint8_t* const mine = lds + (threadIdx.x >> 6) * kD * kColBytes;
   auto issue = [&](int i, auto bc) {
@@ -225,8 +232,8 @@ __global__ __launch_bounds__(64 * kGvWaves) void w4a16_gemv_kernel(W4A16Params p
 }  // namespace
 
 hipError_t w4a16_gemv_launch(bool bf16, const W4A16Params& p, hipStream_t stream) {
-  // two waves per SIMD, at least one column per wave, at most 64 columns per wave
-  const int waves = std::max(std::min(8 * std::max(p.cus, 1), p.N), (p.N + 63) / 64);
+  // kGvWavesPerSimd waves per SIMD, at least one column per wave, at most 64 columns per wave
+  const int waves = std::max(std::min(4 * kGvWavesPerSimd * std::max(p.cus, 1), p.N), (p.N + 63) / 64);
   const dim3 grid((unsigned)((waves + kGvWaves - 1) / kGvWaves)), block(64 * kGvWaves);
   const int kr = p.K <= 2048 ? 1 : p.K <= 4096 ? 2 : 4;
   const int km = p.M <= 1 ? 1 : p.M <= 2 ? 2 : 4;
