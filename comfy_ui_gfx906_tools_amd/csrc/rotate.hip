@@ -3,14 +3,14 @@
 // order g, nodes/ComfyUI-Gfx906Int4/ops.py:43-105), the activation of the forward must be rotated
 // the same way, y = x_g R^T per group of g along K. Instead of the reference's fp32 matmul
 // (ops.py:176-179) this pass computes, per row, y_g = H (signs * x_g) / sqrt(g) with a fast
-// Walsh-Hadamard transform in registers and lane shuffles, and writes y directly as the row-scaled
+// Walsh-Hadamard transform in registers and DPP lane moves, and writes y directly as the row-scaled
 // fp16 operand of the W4A16 GEMM (x16 = y * 2^-e, row_scale = 2^e, max |y| * 2^-e in
 // [2^14, 2^15) before the fp16 rounding), so the rotation costs one HBM pass.
 //
 // One 256-thread block per row; thread t holds elements 8t + 2048 r (r < R). Butterfly strides
 // 1, 2, 4 are inside a thread's 8 values, strides 8 .. g/2 pair thread t with t ^ (stride / 8)
-// (within one wave: a group spans g / 8 <= 16 aligned threads). K % g == 0, so a group is either
-// wholly inside the row or wholly past it; the shuffles run unconditionally on every lane.
+// by DPP moves (a group spans g / 8 <= 16 aligned threads: within one 16-lane DPP row). K % g == 0,
+// so a group is either wholly inside the row or wholly past it; the exchanges run on every lane.
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -37,6 +37,21 @@ __device__ __forceinline__ void load8_row(const void* p, size_t i, float (&v)[8]
       v[2 * e + 1] = DT == kBF16 ? bf16_bits_to_f32(word >> 16) : f16_bits_to_f32(word >> 16);
     }
   }
+}
+
+// Value of lane t ^ D (D = 1, 2, 4, 8; within a 16-lane DPP row) by DPP moves, no LDS round trip:
+// xor 1 and xor 2 are quad permutations; xor 4 = (xor 7: row_half_mirror) then (xor 3: quad
+// [3,2,1,0]); xor 8 = (xor 15: row_mirror) then (xor 7: row_half_mirror).
+template <int kCtrl>
+__device__ __forceinline__ float dpp_mov(float v) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), kCtrl, 0xF, 0xF, false));
+}
+template <int D>
+__device__ __forceinline__ float lane_xor(float v) {
+  if constexpr (D == 1) return dpp_mov<0xB1>(v);
+  else if constexpr (D == 2) return dpp_mov<0x4E>(v);
+  else if constexpr (D == 4) return dpp_mov<0x1B>(dpp_mov<0x141>(v));
+  else return dpp_mov<0x141>(dpp_mov<0x140>(v));
 }
 
 template <int XDT, int G, int R>
@@ -77,15 +92,17 @@ __global__ __launch_bounds__(256) void rotate_rows_to_f16_kernel(const void* __r
         }
     // strides 8 .. G/2 across threads t and t ^ d, d = stride / 8: the lower thread keeps a + b,
     // the upper one a - b (a = the lower thread's value)
+    static_for<0, 4>([&](auto sc) {
+      constexpr int d = 1 << decltype(sc)::value;
+      if constexpr (d < G / 8) {
+        const bool upper = (t & d) != 0;
 #pragma unroll
-    for (int d = 1; d < G / 8; d <<= 1) {
-      const bool upper = (t & d) != 0;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float other = __shfl_xor(v[r][e], d, kWave);
-        v[r][e] = upper ? other - v[r][e] : v[r][e] + other;
+        for (int e = 0; e < 8; ++e) {
+          const float other = lane_xor<d>(v[r][e]);
+          v[r][e] = upper ? other - v[r][e] : v[r][e] + other;
+        }
       }
-    }
+    });
 #pragma unroll
     for (int e = 0; e < 8; ++e) {
       v[r][e] *= inv_sqrt_g;
