@@ -4,12 +4,13 @@
 // kernel, but the products run on v_mfma_f32_16x16x32_{bf16,f16}, whose 16 columns hold up to 16
 // activation rows, so the VALU work per weight does not grow with M.
 //
-// * A workgroup owns 32 output columns (two blocks of 16) for all M rows; its 8 waves split K
-//   into 8 slices of gw quant groups (gw = 4 ceil(G / 32) <= 16) and sum their partial results
-//   through LDS at the end, in wave order (deterministic).
-// * Every load is issued at the start, nothing is recycled: each wave DMAs its 2 x 16 columns x
-//   gw groups of packed weights (8 KiB) and their scales (2 KiB) into a wave-private LDS region
-//   and holds its activation slice (16 rows x gw groups, 16 B per lane and group) in registers.
+// * A workgroup owns B blocks of 16 output columns for all M rows (B = 1 for M <= 8, 2 above);
+//   its 8 waves split K into 8 slices of gw quant groups (gw = 4 ceil(G / 32) <= 16) and sum
+//   their partial results through LDS at the end, in wave order (deterministic).
+// * Every load is issued at the start, nothing is recycled: each wave DMAs its B x 16 columns x
+//   gw groups of packed weights (4 KiB per block) and their scales (1 KiB per block) into a
+//   wave-private LDS region and holds its activation slice (16 rows x gw groups, 16 B per lane
+//   and group) in registers.
 //   The whole weight matrix is in flight from the first microseconds, which is what a one-shot
 //   read of a few tens of MB needs to approach the HBM rate.
 // * Per group t: A = the 16 activation rows of its 32 K, B = the 16 columns' weights as exact
@@ -32,16 +33,17 @@ namespace qlinear {
 
 namespace {
 
-constexpr int kSkWaves = 8;                                // K slices per workgroup
-constexpr int kSkBlocks = 2;                               // 16-column blocks per workgroup
-constexpr int kSkMaxGW = 16;                               // quant groups per wave
-constexpr int kSkColBytes = kSkMaxGW * 16;                 // one column's slice of packed weights
-constexpr int kSkWBytes = kSkBlocks * 16 * kSkColBytes;    // 8 KiB of weights per wave
-constexpr int kSkSBytes = kSkBlocks * 16 * kSkMaxGW * 4;   // 2 KiB of scales per wave
-constexpr int kSkWaveBytes = kSkWBytes + kSkSBytes;
+constexpr int kSkWaves = 8;                 // K slices per workgroup
+constexpr int kSkMaxGW = 16;                // quant groups per wave
+constexpr int kSkColBytes = kSkMaxGW * 16;  // one column's slice of packed weights
 
-template <bool kBf16>
+// kSkBlocks 16-column blocks per workgroup: 1 for up to 8 rows (twice the workgroups in flight),
+// 2 above (the per-group E pass and activation loads shared by twice the columns)
+template <bool kBf16, int kSkBlocks>
 __global__ __launch_bounds__(64 * kSkWaves) void w4a16_skinny_kernel(W4A16Params p) {
+  constexpr int kSkWBytes = kSkBlocks * 16 * kSkColBytes;   // 4 KiB of weights per wave and block
+  constexpr int kSkSBytes = kSkBlocks * 16 * kSkMaxGW * 4;  // 1 KiB of scales per wave and block
+  constexpr int kSkWaveBytes = kSkWBytes + kSkSBytes;
   __shared__ __attribute__((aligned(1024))) uint8_t lds[kSkWaves * kSkWaveBytes];
   const int lane = threadIdx.x & 63;
   const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -156,9 +158,11 @@ __global__ __launch_bounds__(64 * kSkWaves) void w4a16_skinny_kernel(W4A16Params
 #pragma unroll
   for (int b = 0; b < kSkBlocks; ++b) *(f32x4*)(mine + (b * 64 + lane) * 16) = acc[b];
   __syncthreads();
-  {
+  constexpr int kCols = 16 * kSkBlocks;
+  static_assert(16 * kCols <= 64 * kSkWaves, "one output per thread");
+  if (threadIdx.x < 16 * kCols) {  // no barrier below
     const int tid = threadIdx.x;
-    const int m = tid >> 5, nl = tid & 31;  // 16 rows x 32 columns, one output per thread
+    const int m = tid / kCols, nl = tid % kCols;  // 16 rows x kCols columns, one output per thread
     const int b = nl >> 4;
     const int l = 16 * (m >> 2) + (nl & 15), i = m & 3;
     float v = 0.0f;
@@ -173,15 +177,20 @@ __global__ __launch_bounds__(64 * kSkWaves) void w4a16_skinny_kernel(W4A16Params
   }
 }
 
+template <int kSkBlocks>
+hipError_t skinny_launch_b(bool bf16, const W4A16Params& p, hipStream_t stream) {
+  const dim3 grid((unsigned)((p.N + 16 * kSkBlocks - 1) / (16 * kSkBlocks))), block(64 * kSkWaves);
+  if (bf16)
+    hipLaunchKernelGGL((w4a16_skinny_kernel<true, kSkBlocks>), grid, block, 0, stream, p);
+  else
+    hipLaunchKernelGGL((w4a16_skinny_kernel<false, kSkBlocks>), grid, block, 0, stream, p);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t w4a16_skinny_launch(bool bf16, const W4A16Params& p, hipStream_t stream) {
-  const dim3 grid((unsigned)((p.N + 16 * kSkBlocks - 1) / (16 * kSkBlocks))), block(64 * kSkWaves);
-  if (bf16)
-    hipLaunchKernelGGL(w4a16_skinny_kernel<true>, grid, block, 0, stream, p);
-  else
-    hipLaunchKernelGGL(w4a16_skinny_kernel<false>, grid, block, 0, stream, p);
-  return hipGetLastError();
+  return p.M <= 8 ? skinny_launch_b<1>(bf16, p, stream) : skinny_launch_b<2>(bf16, p, stream);
 }
 
 }  // namespace qlinear

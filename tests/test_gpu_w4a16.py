@@ -340,12 +340,12 @@ def test_w4a16_gemv_16bit_out_gelu_and_row_scale(out_dtype):
 SKINNY_CFG = 8
 
 
-@pytest.mark.parametrize("M", [1, 5, 16])
+@pytest.mark.parametrize("M", [1, 5, 8, 9, 16])
 @pytest.mark.parametrize("N,K", [(1, 128), (33, 256), (100, 4096), (257, 3072), (64, 384)])
 @pytest.mark.parametrize("xdt", [torch.bfloat16, torch.float16])
 def test_w4a16_skinny_vs_oracle(M, N, K, xdt):
-    """Configuration 8 (M <= 16, MFMA on exact codes, K split over 8 waves): ragged N (columns past
-    N in the last workgroup), K slices of 4 to 16 groups with idle waves (K = 128: one slice), bias,
+    """Configuration 8 (M <= 16, MFMA on exact codes, K split over 8 waves; one 16-column block per
+    workgroup up to M = 8, two above): ragged N (columns past N in the last workgroup), K slices of 4 to 16 groups with idle waves (K = 128: one slice), bias,
     fp32 out; deterministic and within 2e-4 of the fp64 oracle (exact products, fp32 sums)."""
     print(f"case skinny M={M} N={N} K={K} x={xdt}", flush=True)
     x, wq, ws = seeded_linear(M, N, K, seed=11 * M + N + K, x_dtype=xdt)
@@ -367,25 +367,27 @@ def test_w4a16_skinny_rejects_unsupported_shapes(M, K, msg):
 
 def test_w4a16_skinny_exact_on_integer_grid():
     """Integer x, codes in [-8, 7], power-of-two scales: every partial sum is exact in fp32, so the
-    MFMA kernel must equal the fp64 oracle exactly (both dtypes, all 16 rows)."""
-    M, N, K = 16, 70, 1024
+    MFMA kernel must equal the fp64 oracle exactly (both dtypes; 8 rows on one-block workgroups,
+    16 rows on two-block ones)."""
+    N, K = 70, 1024
     g = np.random.default_rng(43)
     codes = g.integers(-8, 8, (N, K))
     nib = (codes & 0xF).astype(np.uint8)
     packed = (nib[:, 0::2] | (nib[:, 1::2] << 4)).view(np.int8)
     scale = (2.0 ** g.integers(-6, 0, (N, K // 32))).astype(np.float32)
-    for xdt in (torch.bfloat16, torch.float16):
-        x = torch.from_numpy(g.integers(-4, 5, (M, K)).astype(np.float32)).to(xdt)
-        y = to_np_f32(_run_cfg(x, torch.from_numpy(packed), torch.from_numpy(scale), cfg=SKINNY_CFG))
-        ref = orc.w4a16_reference(to_np_f32(x), packed, scale)
-        assert np.array_equal(y.astype(np.float64), ref), f"{xdt}: max abs diff {np.abs(y - ref).max()}"
+    for M in (8, 16):
+        for xdt in (torch.bfloat16, torch.float16):
+            x = torch.from_numpy(g.integers(-4, 5, (M, K)).astype(np.float32)).to(xdt)
+            y = to_np_f32(_run_cfg(x, torch.from_numpy(packed), torch.from_numpy(scale), cfg=SKINNY_CFG))
+            ref = orc.w4a16_reference(to_np_f32(x), packed, scale)
+            assert np.array_equal(y.astype(np.float64), ref), f"M={M} {xdt}: max abs diff {np.abs(y - ref).max()}"
 
 
 @pytest.mark.parametrize("out_dtype", [torch.bfloat16, torch.float16])
 def test_w4a16_skinny_16bit_out_gelu_and_row_scale(out_dtype):
     """16-bit outputs (1 ulp + gate), the fused GELU (1 ulp of the exact GELU of the plain output),
     and fp16 x staged by rows_to_f16 with its row scale, through configuration 8 and the automatic
-    choice (which takes configuration 8 for 4 < M <= 16)."""
+    choice (which takes configuration 8 for 2 <= M <= 16)."""
     from comfy_ui_gfx906_tools_amd import _lib as L
     M, N, K = 12, 300, 3072
     x, wq, ws = seeded_linear(M, N, K, seed=53)
