@@ -128,8 +128,23 @@ bool skinny_fits(int x_dtype, int64_t M, int64_t N, int64_t K) {
          (x_dtype == QL_BF16 || x_dtype == QL_F16);
 }
 
+// 16-column blocks per workgroup of the skinny kernel: the largest B whose grid is one round of
+// workgroups over more than half the CUs, cus / 2 < ceil(N / 16B) <= cus; where none is, one block
+// up to 8 rows and two above. A/B on MI355X (us per call, K = 3072 unless noted; B = 1 / 2 / 3):
+// N = 10240, K = 4096, M = 16: - / 15.1 / 12.3, M = 4: 10.7 / 11.5 / 10.6; N = 12288, M = 16:
+// - / 12.5 / 10.8; N = 6144, M = 4: 6.6 / 6.3 / 7.4; N = 3072, M = 4: 4.75 / 5.75 / -;
+// N = 18432, M = 16: - / 17.4 / 19.3.
+int skinny_blocks(int64_t M, int64_t N, int cus) {
+  for (int b = kSkinnyMaxBlocks; b >= 1; --b) {
+    const int64_t wg = (N + 16 * b - 1) / (16 * b);
+    if (2 * wg > cus && wg <= cus) return b;
+  }
+  return M <= 8 ? 1 : 2;
+}
+
 // One row: the VALU kernel (8.8 us vs 10.6 us at K=4096 N=10240); 2-16 rows: the MFMA kernel
-// (4 rows: 10.9 us vs 14.9 us; 16 rows: 14.5 us vs 22.6 us for the 16-row tile kernel).
+// (4 rows: 10.6 us vs 14.9 us; 16 rows: 12.3 us vs 22.6 us for the 16-row tile kernel, same
+// shape).
 // QL_W4A16_BF16_MFMA asks for the reference's bf16-rounded weights, which only the tile kernels
 // compute; 7 and 8 use the exact codes and are skipped then.
 int w4a16_cfg_for(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, int flags, int cus) {
@@ -155,7 +170,7 @@ W4A16Plan plan_w4a16(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, i
     pl.stages = 1;
   } else if (pl.cfg == kCfgSkinny) {
     pl.BM = 16;
-    pl.BN = 32;
+    pl.BN = 16 * skinny_blocks(M, N, cus);
     pl.stages = 1;
   } else if (is_tile256(pl.cfg)) {
     pl.BM = pl.BN = 256;
@@ -325,7 +340,7 @@ int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const float* r
   p.ksplit = pl.ksplit;
   const bool bf16_mfma = x_dtype == QL_BF16 && !pl.prepass;
   const hipError_t e = pl.cfg == kCfgGemv     ? w4a16_gemv_launch(x_dtype == QL_BF16, p, (hipStream_t)stream)
-                       : pl.cfg == kCfgSkinny ? w4a16_skinny_launch(x_dtype == QL_BF16, p, (hipStream_t)stream)
+                       : pl.cfg == kCfgSkinny ? w4a16_skinny_launch(x_dtype == QL_BF16, pl.BN / 16, p, (hipStream_t)stream)
                        : is_tile256(pl.cfg)
                            ? w4a16_tile256_launch(pl.cfg - kCfgTile256, bf16_mfma, p, (hipStream_t)stream)
                            : w4a16_launch(pl.cfg, bf16_mfma, p, (hipStream_t)stream);

@@ -46,13 +46,13 @@ hipError_t w4a16_launch(int cfg, bool bf16, const W4A16Params& p, hipStream_t st
 constexpr int kTile256Variants = 3;
 hipError_t w4a16_tile256_launch(int variant, bool bf16, const W4A16Params& p, hipStream_t stream);
 // Activation rows up to 4, bf16 / fp16 x as is, K <= 8192 and M * K <= 16384 (w4a16_gemv.hip):
-// VALU dot products on exact integer codes, columns streamed by about two waves per SIMD.
+// VALU dot products on exact integer codes, columns streamed by four waves per SIMD.
 constexpr int kGemvMaxM = 4, kGemvMaxK = 8192, kGemvMaxMK = 16384;
 hipError_t w4a16_gemv_launch(bool bf16, const W4A16Params& p, hipStream_t stream);
-// MFMA kernel for M <= 16 (w4a16_skinny.hip): 32 columns per workgroup, K split over its 8
-// waves; K % 128 == 0, K <= 4096.
-constexpr int kSkinnyMaxM = 16, kSkinnyMaxK = 4096;
-hipError_t w4a16_skinny_launch(bool bf16, const W4A16Params& p, hipStream_t stream);
+// MFMA kernel for M <= 16 (w4a16_skinny.hip): `blocks` (1-3) blocks of 16 columns per workgroup,
+// K split over its 8 waves; K % 128 == 0, K <= 4096.
+constexpr int kSkinnyMaxM = 16, kSkinnyMaxK = 4096, kSkinnyMaxBlocks = 3;
+hipError_t w4a16_skinny_launch(bool bf16, int blocks, const W4A16Params& p, hipStream_t stream);
 hipError_t rows_to_scaled_f16_launch(int dtype, const void* x, void* x16, float* row_scale, int64_t M,
                                      int64_t K, hipStream_t stream);
 

@@ -4,9 +4,11 @@
 // kernel, but the products run on v_mfma_f32_16x16x32_{bf16,f16}, whose 16 columns hold up to 16
 // activation rows, so the VALU work per weight does not grow with M.
 //
-// * A workgroup owns B blocks of 16 output columns for all M rows (B = 1 for M <= 8, 2 above);
-//   its 8 waves split K into 8 slices of gw quant groups (gw = 4 ceil(G / 32) <= 16) and sum
-//   their partial results through LDS at the end, in wave order (deterministic).
+// * A workgroup owns B blocks of 16 output columns for all M rows (B = 1, 2 or 3, chosen by the
+//   caller from N and the CU count); its 8 waves split K into 8 slices of gw quant groups
+//   (gw = 4 ceil(G / 32) <= 16) and sum their partial results through LDS at the end, in wave
+//   order (deterministic). Every workgroup reads all of x (M K 2 bytes, from L2), so larger B
+//   means less x traffic per weight byte; B = 3 takes 120 KiB of LDS (one workgroup per CU).
 // * Every load is issued at the start, nothing is recycled: each wave DMAs its B x 16 columns x
 //   gw groups of packed weights (4 KiB per block) and their scales (1 KiB per block) into a
 //   wave-private LDS region and holds its activation slice (16 rows x gw groups, 16 B per lane
@@ -37,8 +39,7 @@ constexpr int kSkWaves = 8;                 // K slices per workgroup
 constexpr int kSkMaxGW = 16;                // quant groups per wave
 constexpr int kSkColBytes = kSkMaxGW * 16;  // one column's slice of packed weights
 
-// kSkBlocks 16-column blocks per workgroup: 1 for up to 8 rows (twice the workgroups in flight),
-// 2 above (the per-group E pass and activation loads shared by twice the columns)
+// kSkBlocks 16-column blocks per workgroup (1-3)
 template <bool kBf16, int kSkBlocks>
 __global__ __launch_bounds__(64 * kSkWaves) void w4a16_skinny_kernel(W4A16Params p) {
   constexpr int kSkWBytes = kSkBlocks * 16 * kSkColBytes;   // 4 KiB of weights per wave and block
@@ -159,10 +160,8 @@ __global__ __launch_bounds__(64 * kSkWaves) void w4a16_skinny_kernel(W4A16Params
   for (int b = 0; b < kSkBlocks; ++b) *(f32x4*)(mine + (b * 64 + lane) * 16) = acc[b];
   __syncthreads();
   constexpr int kCols = 16 * kSkBlocks;
-  static_assert(16 * kCols <= 64 * kSkWaves, "one output per thread");
-  if (threadIdx.x < 16 * kCols) {  // no barrier below
-    const int tid = threadIdx.x;
-    const int m = tid / kCols, nl = tid % kCols;  // 16 rows x kCols columns, one output per thread
+  for (int tid = threadIdx.x; tid < 16 * kCols; tid += 64 * kSkWaves) {  // no barrier below
+    const int m = tid / kCols, nl = tid % kCols;  // 16 rows x kCols columns
     const int b = nl >> 4;
     const int l = 16 * (m >> 2) + (nl & 15), i = m & 3;
     float v = 0.0f;
@@ -189,8 +188,12 @@ hipError_t skinny_launch_b(bool bf16, const W4A16Params& p, hipStream_t stream) 
 
 }  // namespace
 
-hipError_t w4a16_skinny_launch(bool bf16, const W4A16Params& p, hipStream_t stream) {
-  return p.M <= 8 ? skinny_launch_b<1>(bf16, p, stream) : skinny_launch_b<2>(bf16, p, stream);
+hipError_t w4a16_skinny_launch(bool bf16, int blocks, const W4A16Params& p, hipStream_t stream) {
+  switch (blocks) {
+    case 1: return skinny_launch_b<1>(bf16, p, stream);
+    case 2: return skinny_launch_b<2>(bf16, p, stream);
+    default: return skinny_launch_b<3>(bf16, p, stream);
+  }
 }
 
 }  // namespace qlinear

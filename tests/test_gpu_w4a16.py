@@ -358,6 +358,24 @@ def test_w4a16_skinny_vs_oracle(M, N, K, xdt):
     assert err <= 2e-4, f"max rel err {err:.3e}"
 
 
+@pytest.mark.parametrize("M,N,K", [(4, 5000, 1024), (16, 5000, 1024), (3, 6200, 3072), (16, 6200, 3072),
+                                   (9, 12288, 4096), (16, 18432, 3072), (2, 3072, 3072)])
+def test_w4a16_skinny_block_counts_vs_oracle(M, N, K):
+    """The planner's choice of 16-column blocks per workgroup (on a 256-CU device: N = 5000 -> 2
+    blocks, 157 workgroups; 6200 and 12288 -> 3 blocks, 130 and 256 workgroups; 18432 -> 2 above 8
+    rows; 3072 -> 1), ragged last workgroups included: deterministic and within 2e-4 of the fp64
+    oracle, as for the other skinny shapes."""
+    print(f"case skinny blocks M={M} N={N} K={K}", flush=True)
+    x, wq, ws = seeded_linear(M, N, K, seed=5 * M + N + K)
+    bias = torch.randn(N, generator=torch.Generator().manual_seed(N))
+    y1 = _run_cfg(x, wq, ws, bias, cfg=SKINNY_CFG)
+    y2 = _run_cfg(x, wq, ws, bias)
+    assert torch.equal(y1, y2), "automatic choice differs from configuration 8, or not deterministic"
+    ref = orc.w4a16_reference(to_np_f32(x), wq.numpy(), ws.numpy(), bias.numpy())
+    err = rel_max_err(to_np_f32(y1), ref)
+    assert err <= 2e-4, f"max rel err {err:.3e}"
+
+
 @pytest.mark.parametrize("M,K,msg", [(17, 256, "M <= 16"), (4, 160, "K % 128 == 0"), (4, 8192, "K <= 4096")])
 def test_w4a16_skinny_rejects_unsupported_shapes(M, K, msg):
     x, wq, ws = seeded_linear(M, 8, K, seed=3)
@@ -367,15 +385,15 @@ def test_w4a16_skinny_rejects_unsupported_shapes(M, K, msg):
 
 def test_w4a16_skinny_exact_on_integer_grid():
     """Integer x, codes in [-8, 7], power-of-two scales: every partial sum is exact in fp32, so the
-    MFMA kernel must equal the fp64 oracle exactly (both dtypes; 8 rows on one-block workgroups,
-    16 rows on two-block ones)."""
-    N, K = 70, 1024
+    MFMA kernel must equal the fp64 oracle exactly (both dtypes; on a 256-CU device N = 70 runs on
+    one-block workgroups at 8 rows and two-block ones at 16, N = 6200 on three-block ones)."""
+    K = 1024
     g = np.random.default_rng(43)
-    codes = g.integers(-8, 8, (N, K))
-    nib = (codes & 0xF).astype(np.uint8)
-    packed = (nib[:, 0::2] | (nib[:, 1::2] << 4)).view(np.int8)
-    scale = (2.0 ** g.integers(-6, 0, (N, K // 32))).astype(np.float32)
-    for M in (8, 16):
+    for M, N in ((8, 70), (16, 70), (16, 6200)):
+        codes = g.integers(-8, 8, (N, K))
+        nib = (codes & 0xF).astype(np.uint8)
+        packed = (nib[:, 0::2] | (nib[:, 1::2] << 4)).view(np.int8)
+        scale = (2.0 ** g.integers(-6, 0, (N, K // 32))).astype(np.float32)
         for xdt in (torch.bfloat16, torch.float16):
             x = torch.from_numpy(g.integers(-4, 5, (M, K)).astype(np.float32)).to(xdt)
             y = to_np_f32(_run_cfg(x, torch.from_numpy(packed), torch.from_numpy(scale), cfg=SKINNY_CFG))
