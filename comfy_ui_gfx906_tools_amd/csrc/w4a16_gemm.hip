@@ -388,10 +388,12 @@ __global__ __launch_bounds__(256) void w4a16_reduce_kernel(W4A16Params p, int BM
 
 // x [M, K] (fp32 / fp16 / bf16) -> x16 [M, K] fp16 scaled by 2^-e_m per row, row_scale[m] = 2^e_m,
 // with e_m chosen so that max |x16| lies in [2^14, 2^15): every bf16 value maps exactly (fp16
-// keeps 11 mantissa bits), and no row can overflow fp16. One workgroup per row; 8 elements per
-// thread and step (16-byte loads for 16-bit inputs), the row read twice (max, then convert; the
-// second read hits L2).
-template <int DT>
+// keeps 11 mantissa bits), and no row can overflow fp16. One workgroup per row, 8 elements per
+// thread and step (16-byte loads for 16-bit inputs). R > 0 (K <= 2048 R): thread t holds elements
+// 8t + 2048 r (r < R) in registers, all R loads issued before the first use, the row read once.
+// R = 0 (longer rows): a strided loop, the row read twice (max, then convert; the second read
+// hits L2).
+template <int DT, int R>
 __global__ __launch_bounds__(256) void rows_to_scaled_f16_kernel(const void* __restrict__ x,
                                                                  _Float16* __restrict__ x16,
                                                                  float* __restrict__ row_scale, int K) {
@@ -418,33 +420,85 @@ __global__ __launch_bounds__(256) void rows_to_scaled_f16_kernel(const void* __r
       }
     }
   };
-  float amax = 0.0f;
-  for (int k = threadIdx.x * 8; k < K; k += 256 * 8) {
-    float v[8];
-    load8(k, v);
-#pragma unroll
-    for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
-  }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, kWave));
-  if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
-  __syncthreads();
-  amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  int e = 0;
-  if (amax > 0.0f && amax <= 3.0e38f) {
-    int E;
-    frexpf(amax, &E);  // amax = f * 2^E, f in [0.5, 1)
-    e = E - 15;
-  }
-  if (threadIdx.x == 0) row_scale[row] = ldexpf(1.0f, e);
-  for (int k = threadIdx.x * 8; k < K; k += 256 * 8) {
-    float v[8];
-    load8(k, v);
+  auto store8 = [&](int k, const float (&v)[8], int e) {
     u32x4 out;
 #pragma unroll
     for (int q = 0; q < 4; ++q) out[q] = pack2_f16(ldexpf(v[2 * q], -e), ldexpf(v[2 * q + 1], -e));
     *(u32x4*)(x16 + base + k) = out;
+  };
+  auto row_exponent = [&](float amax) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) amax = fmaxf(amax, __shfl_xor(amax, off, kWave));
+    if ((threadIdx.x & 63) == 0) red[threadIdx.x >> 6] = amax;
+    __syncthreads();
+    amax = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+    int e = 0;
+    if (amax > 0.0f && amax <= 3.0e38f) {
+      int E;
+      frexpf(amax, &E);  // amax = f * 2^E, f in [0.5, 1)
+      e = E - 15;
+    }
+    if (threadIdx.x == 0) row_scale[row] = ldexpf(1.0f, e);
+    return e;
+  };
+  float amax = 0.0f;
+  if constexpr (R > 0) {
+    float v[R][8];
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int k = threadIdx.x * 8 + 2048 * r;
+      if (k < K) {
+        load8(k, v[r]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[r][e] = 0.0f;
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < R; ++r)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[r][e]));
+    const int e = row_exponent(amax);
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int k = threadIdx.x * 8 + 2048 * r;
+      if (k < K) store8(k, v[r], e);
+    }
+  } else {
+    for (int k = threadIdx.x * 8; k < K; k += 256 * 8) {
+      float v[8];
+      load8(k, v);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[e]));
+    }
+    const int e = row_exponent(amax);
+    for (int k = threadIdx.x * 8; k < K; k += 256 * 8) {
+      float v[8];
+      load8(k, v);
+      store8(k, v, e);
+    }
   }
+}
+
+template <int DT>
+hipError_t rows_launch_r(const void* x, void* x16, float* row_scale, int64_t M, int64_t K, hipStream_t stream) {
+  const dim3 grid((unsigned)M), block(256);
+  if (K <= 2048)
+    hipLaunchKernelGGL((rows_to_scaled_f16_kernel<DT, 1>), grid, block, 0, stream, x, (_Float16*)x16, row_scale,
+                       (int)K);
+  else if (K <= 4096)
+    hipLaunchKernelGGL((rows_to_scaled_f16_kernel<DT, 2>), grid, block, 0, stream, x, (_Float16*)x16, row_scale,
+                       (int)K);
+  else if (K <= 8192)
+    hipLaunchKernelGGL((rows_to_scaled_f16_kernel<DT, 4>), grid, block, 0, stream, x, (_Float16*)x16, row_scale,
+                       (int)K);
+  else if (K <= 16384)
+    hipLaunchKernelGGL((rows_to_scaled_f16_kernel<DT, 8>), grid, block, 0, stream, x, (_Float16*)x16, row_scale,
+                       (int)K);
+  else
+    hipLaunchKernelGGL((rows_to_scaled_f16_kernel<DT, 0>), grid, block, 0, stream, x, (_Float16*)x16, row_scale,
+                       (int)K);
+  return hipGetLastError();
 }
 
 }  // namespace
@@ -506,22 +560,11 @@ hipError_t w4a16_launch(int cfg, bool bf16, const W4A16Params& p, hipStream_t st
 
 hipError_t rows_to_scaled_f16_launch(int dtype, const void* x, void* x16, float* row_scale, int64_t M,
                                      int64_t K, hipStream_t stream) {
-  const dim3 grid((unsigned)M);
   switch (dtype) {
-    case kF32:
-      hipLaunchKernelGGL(rows_to_scaled_f16_kernel<kF32>, grid, dim3(256), 0, stream, x, (_Float16*)x16, row_scale,
-                         (int)K);
-      break;
-    case kF16:
-      hipLaunchKernelGGL(rows_to_scaled_f16_kernel<kF16>, grid, dim3(256), 0, stream, x, (_Float16*)x16, row_scale,
-                         (int)K);
-      break;
-    default:
-      hipLaunchKernelGGL(rows_to_scaled_f16_kernel<kBF16>, grid, dim3(256), 0, stream, x, (_Float16*)x16,
-                         row_scale, (int)K);
-      break;
+    case kF32: return rows_launch_r<kF32>(x, x16, row_scale, M, K, stream);
+    case kF16: return rows_launch_r<kF16>(x, x16, row_scale, M, K, stream);
+    default: return rows_launch_r<kBF16>(x, x16, row_scale, M, K, stream);
   }
-  return hipGetLastError();
 }
 
 }  // namespace qlinear
