@@ -24,7 +24,7 @@ def _staging_reference(x: np.ndarray):
     return x16, scale
 
 
-@pytest.mark.parametrize("K", [32, 2048, 2080, 4096, 6144, 8192, 12288, 16384, 16416, 20480])
+@pytest.mark.parametrize("K", [32, 1024, 1056, 2048, 2080, 3072, 3104, 4096, 6144, 8192, 12288, 16384, 16416, 20480])
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16, torch.float32])
 def test_rows_to_f16_bit_exact(K, dt):
     print(f"case staging K={K} dt={dt}", flush=True)

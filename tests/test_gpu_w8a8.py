@@ -21,7 +21,8 @@ def _lib():
 # the element-wise one
 @pytest.mark.parametrize("M,K,dt", [(1, 64, torch.bfloat16), (7, 3072, torch.bfloat16), (300, 1000, torch.float16),
                                     (64, 4096, torch.float32), (5, 1004, torch.float16), (3, 16392, torch.bfloat16),
-                                    (2, 16384, torch.float32)])
+                                    (2, 16384, torch.float32), (9, 2088, torch.bfloat16), (6, 1536, torch.float32),
+                                    (4, 8192, torch.float16)])
 def test_quantize_int8_per_token_matches_oracle(M, K, dt):
     print(f"case quant8 M={M} K={K} {dt}", flush=True)
     g = torch.Generator().manual_seed(M + K)
