@@ -109,8 +109,12 @@ __device__ __forceinline__ u32x4 dequant8(uint32_t w, float s, float neg8s) {
   u32x4 r;
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
-    const float lo = fmaf((float)((ev >> (8 * b)) & 0xFFu), s, neg8s);
-    const float hi = fmaf((float)((od >> (8 * b)) & 0xFFu), s, neg8s);
+    float lo = fmaf((float)((ev >> (8 * b)) & 0xFFu), s, neg8s);
+    float hi = fmaf((float)((od >> (8 * b)) & 0xFFu), s, neg8s);
+    // fp16: keep the fp32 products in full registers so the pair is packed by one
+    // v_cvt_pk_f16_f32 (as v_cvt_pk_bf16_f32 does for bf16) rather than fused into
+    // v_fma_mix{lo,hi}_f16, whose half-register writes chain each pair's two halves
+    if constexpr (!kBf16) asm volatile("" : "+v"(lo), "+v"(hi));
     r[b] = kBf16 ? pack2_bf16(lo, hi) : pack2_f16(lo, hi);
   }
   return r;
