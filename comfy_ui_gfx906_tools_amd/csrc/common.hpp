@@ -34,11 +34,12 @@ __device__ __forceinline__ uint32_t pack2_bf16(float lo, float hi) {
   v[1] = (__bf16)hi;
   return __builtin_bit_cast(uint32_t, v);
 }
+// One v_cvt_pk_f16_f32 (round to nearest even) for the pair. Converting as a 2-vector also keeps
+// the compiler from fusing a producing fp32 fma into v_fma_mix{lo,hi}_f16, whose half-register
+// writes chain the two halves of the result dword.
 __device__ __forceinline__ uint32_t pack2_f16(float lo, float hi) {
-  f16x2 v;
-  v[0] = (_Float16)lo;
-  v[1] = (_Float16)hi;
-  return __builtin_bit_cast(uint32_t, v);
+  typedef float f32x2_t __attribute__((ext_vector_type(2)));
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, f16x2));
 }
 
 // Read element i of a buffer of dtype code dt as fp32.
@@ -109,12 +110,8 @@ __device__ __forceinline__ u32x4 dequant8(uint32_t w, float s, float neg8s) {
   u32x4 r;
 #pragma unroll
   for (int b = 0; b < 4; ++b) {
-    float lo = fmaf((float)((ev >> (8 * b)) & 0xFFu), s, neg8s);
-    float hi = fmaf((float)((od >> (8 * b)) & 0xFFu), s, neg8s);
-    // fp16: keep the fp32 products in full registers so the pair is packed by one
-    // v_cvt_pk_f16_f32 (as v_cvt_pk_bf16_f32 does for bf16) rather than fused into
-    // v_fma_mix{lo,hi}_f16, whose half-register writes chain each pair's two halves
-    if constexpr (!kBf16) asm volatile("" : "+v"(lo), "+v"(hi));
+    const float lo = fmaf((float)((ev >> (8 * b)) & 0xFFu), s, neg8s);
+    const float hi = fmaf((float)((od >> (8 * b)) & 0xFFu), s, neg8s);
     r[b] = kBf16 ? pack2_bf16(lo, hi) : pack2_f16(lo, hi);
   }
   return r;
