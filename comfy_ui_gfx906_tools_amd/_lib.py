@@ -44,8 +44,9 @@ SIGNATURES = {
     "qlinear_last_error": (ctypes.c_char_p, []),
     "qlinear_abi_version": (_c_int, []),
     "qlinear_w4a16_workspace_bytes": (_c_size_t, [_c_int, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int]),
-    "qlinear_w4a16_gemm": (_c_int, [_c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64,
-                                    _c_i64, _c_int, _c_int, _c_vp, _c_size_t, _c_vp]),
+    "qlinear_w4a16_gemm": (_c_int, [_c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64,
+                                    _c_i64, _c_i64, _c_int, _c_int, _c_vp, _c_size_t, _c_vp]),
+    "qlinear_w4a16_col_scales": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
     "qlinear_rows_to_f16": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
     "qlinear_w4a16_auto_splits": (_c_int, [_c_i64, _c_i64, _c_i64, _c_int]),
     "qlinear_quantize_int4": (_c_int, [_c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
@@ -150,17 +151,55 @@ def rows_to_f16(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     return x16, rs
 
 
+def w4a16_col_scales(w_scale: torch.Tensor) -> torch.Tensor:
+    """Per-column power-of-two factors of the fp16 dequant for w_scale [N, K/32] (fp32 [N]):
+    col[n] = 2^e_n with 8 max|w_scale[n, :]| 2^-e_n in [2^14, 2^15) (include/qlinear.h)."""
+    lib = load_library()
+    w_scale = _dev_tensor(w_scale, "w_scale")
+    if w_scale.dtype != torch.float32 or w_scale.dim() != 2:
+        raise RuntimeError(f"w_scale must be a float32 [N, K/32] tensor, got {w_scale.dtype} {tuple(w_scale.shape)}")
+    N, G = w_scale.shape
+    cs = torch.empty((N,), dtype=torch.float32, device=w_scale.device)
+    with torch.cuda.device(w_scale.device):
+        rc = lib.qlinear_w4a16_col_scales(w_scale.data_ptr(), cs.data_ptr(), N, G * 32, _stream_ptr(w_scale.device))
+    _check(rc, "w4a16_col_scales")
+    return cs
+
+
+def cached_col_scales(w_scale: torch.Tensor) -> torch.Tensor | None:
+    """w4a16_col_scales(w_scale), kept on the w_scale tensor object and recomputed when the tensor
+    is modified in place (torch's version counter), moved, or used from another stream. None for
+    tensors without a version counter (inference-mode tensors): the GEMM then computes the factors
+    in its workspace."""
+    try:
+        version = w_scale._version
+    except RuntimeError:
+        return None
+    stream = _stream_ptr(w_scale.device)
+    hit = getattr(w_scale, "_qlinear_col_scale", None)
+    if hit is not None and hit[0] == version and hit[1] == stream:
+        return hit[2]
+    cs = w4a16_col_scales(w_scale)
+    try:
+        w_scale._qlinear_col_scale = (version, stream, cs)
+    except (AttributeError, RuntimeError):
+        pass
+    return cs
+
+
 def w4a16_gemm(x: torch.Tensor, w_q4: torch.Tensor, w_scale: torch.Tensor, bias: torch.Tensor | None = None,
                out_dtype: torch.dtype | None = None, splits: int = 0, bf16_mfma: bool = False,
                row_scale: torch.Tensor | None = None, config: int | None = None,
-               gelu: bool = False) -> torch.Tensor:
+               gelu: bool = False, col_scale: torch.Tensor | None = None) -> torch.Tensor:
     """y[M, N] = x[M, K] @ dequant(w_q4, w_scale)^T (+ bias) on the gfx950 W4A16 kernel.
     x: fp16/bf16/fp32 [M, K]; w_q4: int8 [N, K/2]; w_scale: fp32 [N, K/32]; bias: out_dtype [N].
     bf16 and fp32 activations go through the exact row-scaled fp16 staging unless bf16_mfma is
     set (then bf16 x meets bf16-rounded weights, the reference's bf16 dequant numerics).
     row_scale (fp16 x only): per-row factor from rows_to_f16, applied in the epilogue.
     config: force kernel configuration 0-6 (include/qlinear.h, QL_W4A16_CFG); None = automatic.
-    gelu: fused GELU-tanh epilogue (QL_W4A16_GELU_TANH): gelu(round(y)), as Linear -> GELU."""
+    gelu: fused GELU-tanh epilogue (QL_W4A16_GELU_TANH): gelu(round(y)), as Linear -> GELU.
+    col_scale: the fp16 dequant's column factors (w4a16_col_scales of this w_scale); None = the
+    GEMM computes them in its workspace."""
     lib = load_library()
     x = _dev_tensor(x, "x")
     w_q4 = _dev_tensor(w_q4, "w_q4")
@@ -197,6 +236,11 @@ def w4a16_gemm(x: torch.Tensor, w_q4: torch.Tensor, w_scale: torch.Tensor, bias:
         if x.dtype != torch.float16 or row_scale.dtype != torch.float32 or row_scale.numel() != M:
             raise RuntimeError(f"row_scale needs float16 x and a float32 [{M}] tensor, got x {x.dtype}, "
                                f"row_scale {row_scale.dtype} {tuple(row_scale.shape)}")
+    if col_scale is not None:
+        col_scale = _dev_tensor(col_scale, "col_scale")
+        if col_scale.dtype != torch.float32 or col_scale.numel() != N or col_scale.device != x.device:
+            raise RuntimeError(f"col_scale must be a float32 [{N}] tensor on {x.device}, got {col_scale.dtype} "
+                               f"{tuple(col_scale.shape)} on {col_scale.device}")
     with torch.cuda.device(x.device):
         stream = _stream_ptr(x.device)
         nbytes = lib.qlinear_w4a16_workspace_bytes(xdt, M, N, K, splits, flags, x.device.index)
@@ -204,6 +248,7 @@ def w4a16_gemm(x: torch.Tensor, w_q4: torch.Tensor, w_scale: torch.Tensor, bias:
         rc = lib.qlinear_w4a16_gemm(xdt, _DTYPE_CODE[out_dtype], x.data_ptr(),
                                     row_scale.data_ptr() if row_scale is not None else None,
                                     w_q4.data_ptr(), w_scale.data_ptr(),
+                                    col_scale.data_ptr() if col_scale is not None else None,
                                     bias.data_ptr() if bias is not None else None, y.data_ptr(), M, N, K, splits,
                                     flags, ws.data_ptr() if ws is not None else None,
                                     ws.numel() if ws is not None else 0, stream)

@@ -70,13 +70,14 @@ int device_cus(int device, int* cus) {
 // Tiles first go one per workgroup ("data-parallel"); when that leaves the last wave of a
 // 1-workgroup-per-CU grid badly filled, the tiles of that last wave are cut into ksplit K
 // pieces instead, chosen to minimise the modelled makespan (in tile-times).
-// Workspace layout: [row scales: M fp32][x16: M x K fp16][partial tiles: fp32]
+// Workspace layout: [row scales: M fp32][column factors: N fp32][x16: M x K fp16][partial tiles: fp32]
 constexpr int kMaxCutTiles = 1 << 16;
 
 struct W4A16Plan {
   int cfg, BM, BN, tiles_m, tiles_n, stages, dp_tiles, ksplit, grid;
-  bool prepass;  // stage x as row-scaled fp16
-  size_t off_row_scale, off_x16, off_partial, total;
+  bool prepass;    // stage x as row-scaled fp16
+  bool col_scaled; // fp16 dequant: per-column power-of-two factors (computed unless the caller gives them)
+  size_t off_row_scale, off_col_scale, off_x16, off_partial, total;
 };
 
 size_t align256(size_t v) { return (v + 255) & ~(size_t)255; }
@@ -164,6 +165,9 @@ W4A16Plan plan_w4a16(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, i
   pl.cfg = forced ? forced - 1 : w4a16_cfg_for(x_dtype, M, N, K, splits, flags, cus);
   const bool direct = pl.cfg == kCfgGemv || pl.cfg == kCfgSkinny;  // 16-bit x read as is
   pl.prepass = !direct && (x_dtype == QL_F32 || (x_dtype == QL_BF16 && !(flags & QL_W4A16_BF16_MFMA)));
+  // the tile kernels round q * s to fp16 unless bf16 x meets bf16 MFMA; the direct kernels apply
+  // the scale in fp32
+  pl.col_scaled = !direct && !(x_dtype == QL_BF16 && (flags & QL_W4A16_BF16_MFMA));
   if (pl.cfg == kCfgGemv) {
     pl.BM = 4;
     pl.BN = 16;
@@ -219,9 +223,10 @@ W4A16Plan plan_w4a16(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, i
                                    ? (size_t)(tiles - pl.dp_tiles) * pl.ksplit * pl.BM * pl.BN * sizeof(float)
                                    : 0;
   pl.off_row_scale = 0;
-  pl.off_x16 = pl.off_row_scale + (pl.prepass ? align256((size_t)M * sizeof(float)) : 0);
+  pl.off_col_scale = pl.off_row_scale + (pl.prepass ? align256((size_t)M * sizeof(float)) : 0);
+  pl.off_x16 = pl.off_col_scale + (pl.col_scaled ? align256((size_t)N * sizeof(float)) : 0);
   pl.off_partial = pl.off_x16 + (pl.prepass ? align256((size_t)M * K * 2) : 0);
-  pl.total = (pl.prepass || partial_bytes) ? pl.off_partial + partial_bytes : 0;
+  pl.total = (pl.prepass || pl.col_scaled || partial_bytes) ? pl.off_partial + partial_bytes : 0;
   return pl;
 }
 
@@ -242,7 +247,7 @@ extern "C" {
 
 const char* qlinear_last_error(void) { return g_last_error.c_str(); }
 
-int qlinear_abi_version(void) { return (1 << 16) | 0; }
+int qlinear_abi_version(void) { return (2 << 16) | 0; }
 
 size_t qlinear_w4a16_workspace_bytes(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, int flags,
                                      int device) {
@@ -262,8 +267,8 @@ int qlinear_w4a16_auto_splits(int64_t M, int64_t N, int64_t K, int device) {
 }
 
 int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const float* row_scale, const void* w_q4,
-                       const float* w_scale, const void* bias, void* y, int64_t M, int64_t N, int64_t K, int splits,
-                       int flags, void* workspace, size_t workspace_bytes, void* stream) {
+                       const float* w_scale, const float* col_scale, const void* bias, void* y, int64_t M, int64_t N,
+                       int64_t K, int splits, int flags, void* workspace, size_t workspace_bytes, void* stream) {
   if (x_dtype != QL_BF16 && x_dtype != QL_F16 && x_dtype != QL_F32)
     return fail(QL_ERR_DTYPE, "x dtype %s (%d) unsupported, expected bfloat16, float16 or float32", dtype_name(x_dtype),
                 x_dtype);
@@ -314,6 +319,17 @@ int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const float* r
   W4A16Params p{};
   p.x = x;
   p.row_scale = row_scale;
+  p.col_scale = nullptr;
+  if (pl.col_scaled) {
+    if (col_scale) {
+      p.col_scale = col_scale;
+    } else {
+      float* cs = (float*)(ws + pl.off_col_scale);
+      const hipError_t e = col_scales_launch(w_scale, cs, N, K / 32, (hipStream_t)stream);
+      if (e != hipSuccess) return fail(QL_ERR_LAUNCH, "column scale launch failed: %s", hipGetErrorString(e));
+      p.col_scale = cs;
+    }
+  }
   if (pl.prepass) {
     float* rs = (float*)(ws + pl.off_row_scale);
     void* x16 = ws + pl.off_x16;
@@ -345,6 +361,17 @@ int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const float* r
                            ? w4a16_tile256_launch(pl.cfg - kCfgTile256, bf16_mfma, p, (hipStream_t)stream)
                            : w4a16_launch(pl.cfg, bf16_mfma, p, (hipStream_t)stream);
   if (e != hipSuccess) return fail(QL_ERR_LAUNCH, "w4a16 launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int qlinear_w4a16_col_scales(const float* w_scale, float* col_scale, int64_t N, int64_t K, void* stream) {
+  if (N < 0 || K < 32 || K % 32 != 0 || N > INT32_MAX / 2 || K > (1 << 22))
+    return fail(QL_ERR_SHAPE, "expected w_scale [N, K/32] with K %% 32 == 0, 32 <= K <= 4194304; got N=%lld K=%lld",
+                (long long)N, (long long)K);
+  if (N == 0) return ok();
+  if (!w_scale || !col_scale) return fail(QL_ERR_ARG, "null w_scale / col_scale pointer");
+  const hipError_t e = col_scales_launch(w_scale, col_scale, N, K / 32, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(QL_ERR_LAUNCH, "col_scales launch failed: %s", hipGetErrorString(e));
   return ok();
 }
 

@@ -42,6 +42,12 @@ __device__ __forceinline__ uint32_t pack2_f16(float lo, float hi) {
   return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){lo, hi}, f16x2));
 }
 
+// 1 / c for a power of two c = 2^e, e in [-126, 126] (the column factors of the fp16 dequant):
+// the exponent field reflected about the bias, one integer subtract and exact.
+__device__ __forceinline__ float pow2_recip(float c) {
+  return __builtin_bit_cast(float, 0x7F000000u - __builtin_bit_cast(uint32_t, c));
+}
+
 // Read element i of a buffer of dtype code dt as fp32.
 __device__ __forceinline__ float read_elem(const void* p, int dt, size_t i) {
   if (dt == kF32) return ((const float*)p)[i];

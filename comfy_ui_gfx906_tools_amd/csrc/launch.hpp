@@ -16,6 +16,10 @@ struct W4A16Params {
   const void* bias;      // [N] out dtype, or null
   void* y;               // [M, N] out dtype
   const float* row_scale;  // [M] power-of-two factor applied in the epilogue, or null
+  // [N] power-of-two factor 2^e_n per output column, or null (tile kernels, fp16 dequant): the
+  // group scales of column n are multiplied by 2^-e_n before the fp16 rounding of q * s and the
+  // epilogue multiplies by 2^e_n, so every column's dequantized weights sit in fp16's normal range
+  const float* col_scale;
   float* partial;        // partial tiles of the cut tiles: (tiles - dp_tiles) * ksplit slots of BM * BN fp32
   int M, N, K;
   int out_dtype;
@@ -55,6 +59,9 @@ constexpr int kSkinnyMaxM = 16, kSkinnyMaxK = 4096, kSkinnyMaxBlocks = 3;
 hipError_t w4a16_skinny_launch(bool bf16, int blocks, const W4A16Params& p, hipStream_t stream);
 hipError_t rows_to_scaled_f16_launch(int dtype, const void* x, void* x16, float* row_scale, int64_t M,
                                      int64_t K, hipStream_t stream);
+// col_scale[n] = 2^e_n with 8 max_g |w_scale[n, g]| * 2^-e_n in [2^14, 2^15), e_n clamped to
+// [-126, 126]; 1 for a column whose scales are all zero or not finite (w4a16_gemm.hip).
+hipError_t col_scales_launch(const float* w_scale, float* col_scale, int64_t N, int64_t groups, hipStream_t stream);
 
 struct W8A8Params {
   const int8_t* xq;      // [M, K]

@@ -31,6 +31,12 @@
 //   reads of s+1 -- the stage's last MFMAs then cover both the barrier and the read latency.
 // * Optional row scales (the fp16 route for bf16 activations): x arrives pre-scaled per row by
 //   2^-e (exact) and the epilogue multiplies by 2^e (exact).
+// * Optional column scales (fp16 dequant): column n's group scales are multiplied by 2^-e_n
+//   (exact) before q * s is rounded to fp16, and the epilogue multiplies by 2^e_n (exact), with
+//   e_n from the column's scales (col_scales_kernel). Weights of any fp32 scale then dequantize
+//   into fp16's normal range instead of overflowing (|s| > 8188) or going subnormal
+//   (|s| < 2^-14). Columns already in range have factor 1, and a wave whose 64 columns all do
+//   takes the plain epilogue (the factors cost nothing for ordinary checkpoints).
 // * Scheduling: every workgroup runs one K range of one tile. The first dp_tiles tiles are
 //   whole (kernel instance kCut = false); each remaining tile is cut into ksplit K ranges
 //   (kCut = true, launched next on the same stream) whose fp32 partials a third kernel sums in
@@ -179,6 +185,20 @@ __global__ __launch_bounds__(64 * kWaves) void w4a16_gemm_kernel(W4A16Params p) 
     for (int fn = 0; fn < WN; ++fn)
       acc[fm][fn] = mfma16<kBf16>(u32x4{0u, 0u, 0u, 0u}, u32x4{0u, 0u, 0u, 0u}, f32x4{0.f, 0.f, 0.f, 0.f});
 
+  // Column factors (fp16 dequant): the lane's weight columns n0 + col0 + 16 fn dequantize with
+  // their group scales times 1 / col_scale[n] (an exact power of two), undone in the epilogue.
+  // Loaded here, ahead of the prologue's loads; csd is formed after the prologue's wait, so the
+  // load's latency hides behind the first stage's.
+  float csv[WN], csd[WN];
+  {
+    const float* cs_p = p.col_scale;
+#pragma unroll
+    for (int fn = 0; fn < WN; ++fn) {
+      const int n = n0 + col0 + 16 * fn;
+      csv[fn] = (cs_p && n < N) ? cs_p[n] : 1.0f;
+    }
+  }
+
   // kNB register sets for the raw weights, rotating with the LDS buffers.
   u32x4 raw[kNB][WN];
   float sc[kNB][WN];
@@ -235,7 +255,10 @@ __global__ __launch_bounds__(64 * kWaves) void w4a16_gemm_kernel(W4A16Params p) 
         // kNB-2 stages ago) complete, the barrier; from here the ring reads the first fragments
         // of s+1, and the MFMAs q .. kQ-1 of this stage cover the barrier and their latency
 #pragma unroll
-        for (int fn = 0; fn < WN; ++fn) bn[fn] = dequant8<kBf16>(raw[k1][fn][0], sc[k1][fn], -8.0f * sc[k1][fn]);
+        for (int fn = 0; fn < WN; ++fn) {
+          sc[k1][fn] *= csd[fn];  // the scales of s+1, each multiplied by its column factor once
+          bn[fn] = dequant8<kBf16>(raw[k1][fn][0], sc[k1][fn], -8.0f * sc[k1][fn]);
+        }
         wait_vmcnt<(kNB - 2) * kLoadsPerStage>();  // this wave's loads of s+1 have landed
         wait_lgkm();                                // its operand reads of buffer k are done
         barrier_no_fence();
@@ -274,7 +297,11 @@ __global__ __launch_bounds__(64 * kWaves) void w4a16_gemm_kernel(W4A16Params p) 
   });
   wait_vmcnt<(kNB - 2) * kLoadsPerStage>();
 #pragma unroll
-  for (int fn = 0; fn < WN; ++fn) bn[fn] = dequant8<kBf16>(raw[0][fn][0], sc[0][fn], -8.0f * sc[0][fn]);
+  for (int fn = 0; fn < WN; ++fn) {
+    csd[fn] = pow2_recip(csv[fn]);
+    sc[0][fn] *= csd[fn];
+    bn[fn] = dequant8<kBf16>(raw[0][fn][0], sc[0][fn], -8.0f * sc[0][fn]);
+  }
   barrier_no_fence();
 #pragma unroll
   for (int d = 0; d < kD; ++d) ar[d] = frag(0, d);
@@ -299,6 +326,7 @@ __global__ __launch_bounds__(64 * kWaves) void w4a16_gemm_kernel(W4A16Params p) 
   int dst_m0 = m0, dst_n0 = n0, dst_M = M, dst_N = N, dst_dtype = p.out_dtype, dst_act = p.act;
   const void* bias = p.bias;
   const float* row_scale = p.row_scale;
+  const float* col_scale = p.col_scale;
   if constexpr (kCut) {
     dst = p.partial + (size_t)g * (BM * BN);
     dst_m0 = 0;
@@ -309,6 +337,7 @@ __global__ __launch_bounds__(64 * kWaves) void w4a16_gemm_kernel(W4A16Params p) 
     dst_act = kActNone;
     bias = nullptr;
     row_scale = nullptr;
+    col_scale = nullptr;
   }
   const bool vec = dst_N % 4 == 0 && ((uintptr_t)dst & 15) == 0;
   float bv[WN][4];
@@ -318,44 +347,65 @@ __global__ __launch_bounds__(64 * kWaves) void w4a16_gemm_kernel(W4A16Params p) 
 #pragma unroll
     for (int e = 0; e < 4; ++e) bv[fn][e] = (bias && n + e < dst_N) ? read_elem(bias, p.out_dtype, n + e) : 0.0f;
   }
+  // The wave's output columns are the columns of its K loop (csd). When every one has factor 1
+  // (ordinary checkpoints) the plain epilogue runs; the choice is uniform over the wave.
+  bool col_one = true;
 #pragma unroll
-  for (int fm = 0; fm < WM; ++fm) {
-    const int m = dst_m0 + fm * 16 + r16;
-    if (m < dst_M) {
-      const float rs = row_scale ? row_scale[m] : 1.0f;
+  for (int fn = 0; fn < WN; ++fn) col_one = col_one && csd[fn] == 1.0f;
+  const bool scaled_cols = col_scale != nullptr && __builtin_amdgcn_ballot_w64(!col_one) != 0;
+  auto store_tile = [&](auto kc) {
+    constexpr bool kColScaled = decltype(kc)::value;
+    float cu[WN][4];
 #pragma unroll
-      for (int fn = 0; fn < WN; ++fn) {
-        const int n = dst_n0 + (wn * WN + fn) * 16 + 4 * j4;
-        float v[4];
+    for (int fn = 0; fn < WN; ++fn) {
+      const int n = dst_n0 + (wn * WN + fn) * 16 + 4 * j4;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          v[e] = acc[fm][fn][e] * rs + bv[fn][e];
-          if (dst_act == kActGeluTanh) v[e] = gelu_tanh(round_to(dst_dtype, v[e]));
-        }
-        const size_t off = (size_t)m * dst_N + n;
-        if (vec && n + 3 < dst_N) {
-          if (dst_dtype == kF32) {
-            *(f32x4*)((float*)dst + off) = f32x4{v[0], v[1], v[2], v[3]};
-          } else {
-            typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-            const bool bf = dst_dtype == kBF16;
-            const u32x2 w = {bf ? pack2_bf16(v[0], v[1]) : pack2_f16(v[0], v[1]),
-                             bf ? pack2_bf16(v[2], v[3]) : pack2_f16(v[2], v[3])};
-            *(u32x2*)((uint16_t*)dst + off) = w;
+      for (int e = 0; e < 4; ++e) cu[fn][e] = (kColScaled && n + e < dst_N) ? col_scale[n + e] : 1.0f;
+    }
+#pragma unroll
+    for (int fm = 0; fm < WM; ++fm) {
+      const int m = dst_m0 + fm * 16 + r16;
+      if (m < dst_M) {
+        const float rs = row_scale ? row_scale[m] : 1.0f;
+#pragma unroll
+        for (int fn = 0; fn < WN; ++fn) {
+          const int n = dst_n0 + (wn * WN + fn) * 16 + 4 * j4;
+          float v[4];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            v[e] = kColScaled ? acc[fm][fn][e] * rs * cu[fn][e] + bv[fn][e] : acc[fm][fn][e] * rs + bv[fn][e];
+            if (dst_act == kActGeluTanh) v[e] = gelu_tanh(round_to(dst_dtype, v[e]));
           }
-        } else {
+          const size_t off = (size_t)m * dst_N + n;
+          if (vec && n + 3 < dst_N) {
+            if (dst_dtype == kF32) {
+              *(f32x4*)((float*)dst + off) = f32x4{v[0], v[1], v[2], v[3]};
+            } else {
+              typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+              const bool bf = dst_dtype == kBF16;
+              const u32x2 w = {bf ? pack2_bf16(v[0], v[1]) : pack2_f16(v[0], v[1]),
+                               bf ? pack2_bf16(v[2], v[3]) : pack2_f16(v[2], v[3])};
+              *(u32x2*)((uint16_t*)dst + off) = w;
+            }
+          } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e)
-            if (n + e < dst_N) write_elem(dst, dst_dtype, off + e, v[e]);
+            for (int e = 0; e < 4; ++e)
+              if (n + e < dst_N) write_elem(dst, dst_dtype, off + e, v[e]);
+          }
         }
       }
+      __builtin_amdgcn_sched_barrier(0);
     }
-    __builtin_amdgcn_sched_barrier(0);
+  };
+  if (scaled_cols) {
+    store_tile(ic<1>{});
+  } else {
+    store_tile(ic<0>{});
   }
 }
 
-// Sums the ksplit fp32 partials of every cut tile in piece order, applies the row scale and the
-// bias, and stores y. Grid: (cut tiles) x (BM*BN / 1024) workgroups of 256 threads, 4 elements
+// Sums the ksplit fp32 partials of every cut tile in piece order, applies the row and column
+// scales and the bias, and stores y. Grid: (cut tiles) x (BM*BN / 1024) workgroups of 256 threads, 4 elements
 // per thread.
 __global__ __launch_bounds__(256) void w4a16_reduce_kernel(W4A16Params p, int BM, int BN) {
   const int tl = blockIdx.y;  // cut tile index
@@ -375,12 +425,22 @@ __global__ __launch_bounds__(256) void w4a16_reduce_kernel(W4A16Params p, int BM
   const int m = tm * BM + idx / BN;
   if (m >= p.M) return;
   const float rs = p.row_scale ? p.row_scale[m] : 1.0f;
+  const int n0 = tn * BN + idx % BN;  // a multiple of 4
+  f32x4 cu = {1.0f, 1.0f, 1.0f, 1.0f};
+  if (p.col_scale) {
+    if (n0 + 3 < p.N) {
+      cu = *(const f32x4*)(p.col_scale + n0);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) cu[e] = n0 + e < p.N ? p.col_scale[n0 + e] : 1.0f;
+    }
+  }
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
-    const int n = tn * BN + idx % BN + e;
+    const int n = n0 + e;
     if (n >= p.N) continue;
     const float bv = p.bias ? read_elem(p.bias, p.out_dtype, n) : 0.0f;
-    float out = v[e] * rs + bv;
+    float out = v[e] * rs * cu[e] + bv;
     if (p.act == kActGeluTanh) out = gelu_tanh(round_to(p.out_dtype, out));
     write_elem(p.y, p.out_dtype, (size_t)m * p.N + n, out);
   }
@@ -480,6 +540,43 @@ __global__ __launch_bounds__(256) void rows_to_scaled_f16_kernel(const void* __r
   }
 }
 
+// Per-column power-of-two factors of the fp16 dequant: one wave per column n. A column whose
+// dequantized weights q s already lie in fp16's normal range for every code (every nonzero |s| >=
+// 2^-14 and 8 max |s| <= 65504) gets 1, so the tile kernels compute exactly what a plain fp16
+// dequant computes; any other column gets 2^e with 8 max |s| 2^-e in [2^14, 2^15) (|q s| <= 8 |s|
+// for codes in [-8, 7]): q s 2^-e is then a normal fp16 number for every code of the column's
+// largest group and overflows for none. e is clamped to [-126, 126] (2^e and 2^-e both normal
+// fp32); a column whose largest scale is not finite gets 1. Four columns per 256-thread
+// workgroup.
+__global__ __launch_bounds__(256) void col_scales_kernel(const float* __restrict__ ws, float* __restrict__ cs, int N,
+                                                         int groups) {
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  if (n >= N) return;
+  const float* row = ws + (size_t)n * groups;
+  float mx = 0.0f, mn = INFINITY;
+  for (int g = lane; g < groups; g += kWave) {
+    const float a = fabsf(row[g]);
+    mx = fmaxf(mx, a);
+    if (a > 0.0f) mn = fminf(mn, a);
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    mx = fmaxf(mx, __shfl_xor(mx, off, kWave));
+    mn = fminf(mn, __shfl_xor(mn, off, kWave));
+  }
+  if (lane == 0) {
+    int e = 0;
+    const bool in_range = mn >= 0x1p-14f && 8.0f * mx <= 65504.0f;
+    if (!in_range && mx > 0.0f && mx <= 3.4028235e38f) {
+      int E;
+      frexpf(mx, &E);  // mx = f 2^E, f in [0.5, 1): 8 mx in [2^(E+2), 2^(E+3))
+      e = min(max(E - 12, -126), 126);
+    }
+    cs[n] = ldexpf(1.0f, e);
+  }
+}
+
 template <int DT>
 hipError_t rows_launch_r(const void* x, void* x16, float* row_scale, int64_t M, int64_t K, hipStream_t stream) {
   const dim3 grid((unsigned)M), block(256);
@@ -565,6 +662,12 @@ hipError_t rows_to_scaled_f16_launch(int dtype, const void* x, void* x16, float*
     case kF16: return rows_launch_r<kF16>(x, x16, row_scale, M, K, stream);
     default: return rows_launch_r<kBF16>(x, x16, row_scale, M, K, stream);
   }
+}
+
+hipError_t col_scales_launch(const float* w_scale, float* col_scale, int64_t N, int64_t groups, hipStream_t stream) {
+  hipLaunchKernelGGL(col_scales_kernel, dim3((unsigned)((N + 3) / 4)), dim3(256), 0, stream, w_scale, col_scale,
+                     (int)N, (int)groups);
+  return hipGetLastError();
 }
 
 }  // namespace qlinear

@@ -22,9 +22,12 @@
 // * LDS swizzles (swz_a, swz_b) make every 16-byte operand read conflict free: activation rows
 //   are 128 B, weight columns 32 B.
 // * Rows past M, columns past N read zeros (buffer range checks); K must be a multiple of 64.
+// * Optional column factors (fp16 dequant, as in w4a16_gemm.hip): column n's scales are read as
+//   s / col_scale[n] and the epilogue multiplies by col_scale[n], both exact powers of two, so the
+//   dequantized weights stay in fp16's normal range for any fp32 scale.
 // * Epilogue: lane (m, h) of an accumulator block holds y[m][n .. n+3] for n = 8b + 4h, b = 0..3
-//   (the transpose of the MFMA's row-major output): bias, optional exact row scale, rounding to
-//   the output dtype, one 8- or 16-byte store per 4 outputs.
+//   (the transpose of the MFMA's row-major output): bias, optional exact row and column scales,
+//   rounding to the output dtype, one 8- or 16-byte store per 4 outputs.
 #include "common.hpp"
 #include "launch.hpp"
 
@@ -228,12 +231,15 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W
   }();
   u32x4 raw[WN], a[WM], b[WN], bn[WN];
   float sc[WN];
+  // Column factors (fp16 dequant): the lane's weight column n dequantizes with its group scales
+  // times 1 / col_scale[n] (an exact power of two), undone in the epilogue.
+  float csd[WN];
   auto first_weights = [&](auto bc) {
     constexpr int bf = decltype(bc)::value;
 #pragma unroll
     for (int i = 0; i < WN; ++i) {
       raw[i] = read_b(bf, i);
-      sc[i] = read_s(bf, i);
+      sc[i] = read_s(bf, i) * csd[i];
     }
   };
   auto stage = [&](auto bc, int s) {
@@ -279,9 +285,22 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W
   };
 
   // ---- prologue: stages 0 and 1 in flight, stage 0 published --------------------------------
+  // The column factors load first; csd is formed after the wait for stage 0, so their latency
+  // hides behind the stage loads.
+  {
+    const float* cs_p = p.col_scale;
+    asm volatile("" : "+s"(cs_p));
+#pragma unroll
+    for (int i = 0; i < WN; ++i) {
+      const int n = n0 + wn * 32 * WN + 32 * i + c32;
+      csd[i] = (cs_p && n < N) ? cs_p[n] : 1.0f;
+    }
+  }
   load_stage(0, 0);
   load_stage(1, 1);
   wait_vmcnt<nL>();
+#pragma unroll
+  for (int i = 0; i < WN; ++i) csd[i] = pow2_recip(csd[i]);
   barrier_no_fence();
   first_weights(ic<0>{});
 #pragma unroll
@@ -297,14 +316,16 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W
   if (s < S) stage(ic<1>{}, s++);
 
   // ---- epilogue ----------------------------------------------------------------------------
-  // v = acc * row_scale + bias; with the GELU epilogue v is first rounded to the output dtype
+  // v = acc * row_scale * col_scale + bias (both scales exact powers of two); with the GELU
+  // epilogue v is first rounded to the output dtype
   // (the unfused sequence's linear output) and then passed through gelu_tanh. Bias and row
   // scales go to registers before any store (y may alias them as far as the compiler knows).
   // (The pointers pass through an empty asm statement so the loads are not hoisted above the K
   // loop, where their registers would be live across it.)
   const void* bias_p = p.bias;
   const float* rs_p = p.row_scale;
-  asm volatile("" : "+s"(bias_p), "+s"(rs_p));
+  const float* cu_p = p.col_scale;
+  asm volatile("" : "+s"(bias_p), "+s"(rs_p), "+s"(cu_p));
   float bv[WN][4][4], rsj[WM];
 #pragma unroll
   for (int i = 0; i < WN; ++i)
@@ -315,6 +336,18 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W
         const int n = n0 + wn * 32 * WN + 32 * i + 8 * bq + 4 * h + e;
         bv[i][bq][e] = (bias_p && n < N) ? read_elem(bias_p, p.out_dtype, n) : 0.0f;
       }
+  // When every column of the tile has factor 1 (ordinary checkpoints) the plain epilogue runs.
+  // Each wave checks all BN columns (BN / 64 per lane), so the choice is uniform over the
+  // workgroup: the 16-bit epilogue below passes workgroup barriers.
+  bool col_one = true;
+  if (cu_p) {
+#pragma unroll
+    for (int e = 0; e < BN / 64; ++e) {
+      const int n = n0 + (BN / 64) * lane + e;
+      col_one = col_one && (n >= N || cu_p[n] == 1.0f);
+    }
+  }
+  const bool scaled_cols = __builtin_amdgcn_ballot_w64(!col_one) != 0;
 #pragma unroll
   for (int j = 0; j < WM; ++j) {
     const int m = m0 + wm * 32 * WM + 32 * j + c32;
@@ -322,10 +355,22 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W
   }
   // The epilogue is instantiated per (activation, output dtype), so that its per-value code has no
   // branches; one uniform dispatch selects the instance.
-  auto epilogue = [&](auto actc, auto odtc) {
+  auto epilogue = [&](auto actc, auto odtc, auto colc) {
     constexpr int kAct = decltype(actc)::value, kOdt = decltype(odtc)::value;
+    constexpr bool kColScaled = decltype(colc)::value;
+    float cu[WN][4][4];
+#pragma unroll
+    for (int i = 0; i < WN; ++i)
+#pragma unroll
+      for (int bq = 0; bq < 4; ++bq)
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int n = n0 + wn * 32 * WN + 32 * i + 8 * bq + 4 * h + e;
+          cu[i][bq][e] = (kColScaled && n < N) ? cu_p[n] : 1.0f;
+        }
     auto value = [&](int i, int j, int bq, int e) {
-      float v = acc[i][j][4 * bq + e] * rsj[j] + bv[i][bq][e];
+      float v = kColScaled ? acc[i][j][4 * bq + e] * rsj[j] * cu[i][bq][e] + bv[i][bq][e]
+                           : acc[i][j][4 * bq + e] * rsj[j] + bv[i][bq][e];
       if constexpr (kAct == kActGeluTanh) v = gelu_tanh(round_to(kOdt, v));
       return v;
     };
@@ -412,16 +457,23 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W
     }
   };
   const bool gelu = p.act == kActGeluTanh;
-  switch (p.out_dtype) {
-    case kF32:
-      gelu ? epilogue(ic<kActGeluTanh>{}, ic<kF32>{}) : epilogue(ic<kActNone>{}, ic<kF32>{});
-      break;
-    case kF16:
-      gelu ? epilogue(ic<kActGeluTanh>{}, ic<kF16>{}) : epilogue(ic<kActNone>{}, ic<kF16>{});
-      break;
-    default:
-      gelu ? epilogue(ic<kActGeluTanh>{}, ic<kBF16>{}) : epilogue(ic<kActNone>{}, ic<kBF16>{});
-      break;
+  auto run = [&](auto colc) {
+    switch (p.out_dtype) {
+      case kF32:
+        gelu ? epilogue(ic<kActGeluTanh>{}, ic<kF32>{}, colc) : epilogue(ic<kActNone>{}, ic<kF32>{}, colc);
+        break;
+      case kF16:
+        gelu ? epilogue(ic<kActGeluTanh>{}, ic<kF16>{}, colc) : epilogue(ic<kActNone>{}, ic<kF16>{}, colc);
+        break;
+      default:
+        gelu ? epilogue(ic<kActGeluTanh>{}, ic<kBF16>{}, colc) : epilogue(ic<kActNone>{}, ic<kBF16>{}, colc);
+        break;
+    }
+  };
+  if (scaled_cols) {
+    run(ic<1>{});
+  } else {
+    run(ic<0>{});
   }
 }
 

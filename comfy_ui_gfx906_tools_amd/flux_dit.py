@@ -100,14 +100,17 @@ def _linear(layer, x, gelu: bool = False, rows: slice | None = None) -> torch.Te
     accept a Staged operand."""
     if _is_engine_linear(layer):
         wq, ws, b = layer.weight_q4, layer.weight_scale, layer.bias
+        # the fp16 dequant's per-column factors, kept with the whole weight (rows slice them)
+        cs = _lib.cached_col_scales(ws) if ws.is_cuda else None
         if rows is not None:
             wq, ws = wq[rows], ws[rows]
             b = b[rows] if b is not None else None
+            cs = cs[rows] if cs is not None else None
         if isinstance(x, Staged):
             if layer.rotation_group:
                 raise RuntimeError("a layer with activation rotation takes a plain activation tensor")
             y = _lib.w4a16_gemm(x.x16, wq, ws, b.to(x.dtype) if b is not None else None, out_dtype=x.dtype,
-                                row_scale=x.row_scale, gelu=gelu)
+                                row_scale=x.row_scale, gelu=gelu, col_scale=cs)
             return y.reshape(*x.lead, wq.shape[0])
         shape = x.shape
         x2 = x.reshape(-1, shape[-1])
@@ -116,10 +119,10 @@ def _linear(layer, x, gelu: bool = False, rows: slice | None = None) -> torch.Te
             g = layer.rotation_group
             if shape[-1] <= ROTATE_FUSED_MAX_K:
                 x16, rs = _lib.rotate_rows_to_f16(x2, get_group_signs(g, x2.device), g)
-                y = _lib.w4a16_gemm(x16, wq, ws, bias, out_dtype=x.dtype, row_scale=rs, gelu=gelu)
+                y = _lib.w4a16_gemm(x16, wq, ws, bias, out_dtype=x.dtype, row_scale=rs, gelu=gelu, col_scale=cs)
                 return y.reshape(*shape[:-1], wq.shape[0])
             x2 = apply_group_rotation(x2.float(), get_group_rotation(shape[-1], g, x2.device), g)
-        y = _lib.w4a16_gemm(x2, wq, ws, bias, out_dtype=x.dtype, gelu=gelu)
+        y = _lib.w4a16_gemm(x2, wq, ws, bias, out_dtype=x.dtype, gelu=gelu, col_scale=cs)
         return y.reshape(*shape[:-1], wq.shape[0])
     w, b = layer.weight, layer.bias
     if rows is not None:

@@ -45,7 +45,7 @@ enum qlinear_status {
 /* Message for the last failing call on this host thread ("" if none). */
 const char* qlinear_last_error(void);
 
-/* ABI version of this header: (major << 16) | minor. */
+/* ABI version of this header: (major << 16) | minor. 2.0: qlinear_w4a16_gemm takes col_scale. */
 int qlinear_abi_version(void);
 
 /* ---------------------------------------------------------------------------------------
@@ -67,9 +67,12 @@ int qlinear_abi_version(void);
  *   K % 32 == 0, K >= 32; M >= 0 (M == 0 launches nothing)
  *   splits    0 = automatic (under-filled last waves are cut into K pieces),
  *             1 = one workgroup per output tile, 2..64 = that many K pieces per tile.
+ *   col_scale [N] fp32 from qlinear_w4a16_col_scales(w_scale), or NULL (then computed into the
+ *             workspace by the call); read only by the tile kernels on the fp16 route.
  *   workspace device memory of qlinear_w4a16_workspace_bytes(...) bytes (NULL when that is 0),
- *             scratch for the fp16 staging copy and split-K partial tiles; no initial contents
- *             needed. Calls sharing one workspace must be ordered (same stream).
+ *             scratch for the fp16 staging copy, the column factors and split-K partial tiles;
+ *             no initial contents needed. Calls sharing one workspace must be ordered (same
+ *             stream).
  * ------------------------------------------------------------------------------------- */
 #define QL_W4A16_BF16_MFMA 1 /* flags bit, see above */
 /* flags bit: GELU (tanh approximation) epilogue, y = gelu(round(x @ W^T + bias)) with the linear's
@@ -93,9 +96,21 @@ size_t qlinear_w4a16_workspace_bytes(int x_dtype, int64_t M, int64_t N, int64_t 
                                      int flags, int device);
 
 int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const float* row_scale,
-                       const void* w_q4, const float* w_scale, const void* bias, void* y,
-                       int64_t M, int64_t N, int64_t K, int splits, int flags, void* workspace,
-                       size_t workspace_bytes, void* stream);
+                       const void* w_q4, const float* w_scale, const float* col_scale,
+                       const void* bias, void* y, int64_t M, int64_t N, int64_t K, int splits,
+                       int flags, void* workspace, size_t workspace_bytes, void* stream);
+
+/* Column factors of the fp16 dequant: col_scale[n] = 2^e_n with 8 * max_g |w_scale[n, g]| * 2^-e_n
+ * in [2^14, 2^15) (e_n clamped to [-126, 126]; 1 for a column whose scales are all 0 or not
+ * finite). The tile kernels (configurations 0-6 on the fp16 route) dequantize column n as
+ * fp16(q * s * 2^-e_n) and multiply the column by 2^e_n in the epilogue, so weights of any fp32
+ * scale keep 11 significant bits without overflow (the reference's bf16 dequant, nodes.py:116,
+ * keeps the full exponent range too); where q * s is a normal fp16 number the result is the
+ * same bit for bit. qlinear_w4a16_gemm computes them into its workspace when col_scale is NULL
+ * (one small launch per call); a caller that keeps them with the weight computes them once here
+ * and passes them in. They depend only on w_scale. K % 32 == 0. No counterpart in the reference. */
+int qlinear_w4a16_col_scales(const float* w_scale, float* col_scale, int64_t N, int64_t K,
+                             void* stream);
 
 /* Staging pass of the fp16 route: x[M,K] (fp32/fp16/bf16, K % 8 == 0) -> x16[M,K] fp16 with
  * row m scaled by 2^-e_m, row_scale[m] = 2^e_m, e_m chosen so max|x16[m,:]| is in [2^14, 2^15)
