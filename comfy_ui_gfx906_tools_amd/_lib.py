@@ -27,6 +27,7 @@ W4A16_BF16_MFMA = 1  # flags: bf16 activations straight into bf16 MFMA (see incl
 W4A16_GELU_TANH = 2  # flags: fused GELU-tanh epilogue
 W4A16_CFG_SHIFT = 8  # flags bits 8-11: forced kernel configuration + 1 (QL_W4A16_CFG)
 W4A16_TILE256 = 4    # configuration id of the 256 x 256, 8-wave kernel
+W4A16_NOALLOC_SCRATCH_BYTES = 32 << 20  # QL_W4A16_NOALLOC_SCRATCH_BYTES
 
 RULE_DIV = 0    # scale = amax / 7        (torch on CPU)
 RULE_RECIP = 1  # scale = amax * fl(1/7)  (torch on GPU; the reference kernel)
@@ -47,6 +48,8 @@ SIGNATURES = {
     "qlinear_w4a16_gemm": (_c_int, [_c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64,
                                     _c_i64, _c_i64, _c_int, _c_int, _c_vp, _c_size_t, _c_vp]),
     "qlinear_w4a16_col_scales": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
+    "qlinear_w4a16_gemm_noalloc": (_c_int, [_c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64,
+                                            _c_i64, _c_i64, _c_int, _c_int, _c_vp]),
     "qlinear_rows_to_f16": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
     "qlinear_w4a16_auto_splits": (_c_int, [_c_i64, _c_i64, _c_i64, _c_int]),
     "qlinear_quantize_int4": (_c_int, [_c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
@@ -190,7 +193,7 @@ def cached_col_scales(w_scale: torch.Tensor) -> torch.Tensor | None:
 def w4a16_gemm(x: torch.Tensor, w_q4: torch.Tensor, w_scale: torch.Tensor, bias: torch.Tensor | None = None,
                out_dtype: torch.dtype | None = None, splits: int = 0, bf16_mfma: bool = False,
                row_scale: torch.Tensor | None = None, config: int | None = None,
-               gelu: bool = False, col_scale: torch.Tensor | None = None) -> torch.Tensor:
+               gelu: bool = False, col_scale: torch.Tensor | None = None, noalloc: bool = False) -> torch.Tensor:
     """y[M, N] = x[M, K] @ dequant(w_q4, w_scale)^T (+ bias) on the gfx950 W4A16 kernel.
     x: fp16/bf16/fp32 [M, K]; w_q4: int8 [N, K/2]; w_scale: fp32 [N, K/32]; bias: out_dtype [N].
     bf16 and fp32 activations go through the exact row-scaled fp16 staging unless bf16_mfma is
@@ -199,7 +202,9 @@ def w4a16_gemm(x: torch.Tensor, w_q4: torch.Tensor, w_scale: torch.Tensor, bias:
     config: force kernel configuration 0-6 (include/qlinear.h, QL_W4A16_CFG); None = automatic.
     gelu: fused GELU-tanh epilogue (QL_W4A16_GELU_TANH): gelu(round(y)), as Linear -> GELU.
     col_scale: the fp16 dequant's column factors (w4a16_col_scales of this w_scale); None = the
-    GEMM computes them in its workspace."""
+    GEMM computes them in its workspace.
+    noalloc: run qlinear_w4a16_gemm_noalloc (the library's static scratch instead of a workspace
+    from torch's allocator; calls needing more than QL_W4A16_NOALLOC_SCRATCH_BYTES raise)."""
     lib = load_library()
     x = _dev_tensor(x, "x")
     w_q4 = _dev_tensor(w_q4, "w_q4")
@@ -243,6 +248,15 @@ def w4a16_gemm(x: torch.Tensor, w_q4: torch.Tensor, w_scale: torch.Tensor, bias:
                                f"{tuple(col_scale.shape)} on {col_scale.device}")
     with torch.cuda.device(x.device):
         stream = _stream_ptr(x.device)
+        if noalloc:
+            rc = lib.qlinear_w4a16_gemm_noalloc(xdt, _DTYPE_CODE[out_dtype], x.data_ptr(),
+                                                row_scale.data_ptr() if row_scale is not None else None,
+                                                w_q4.data_ptr(), w_scale.data_ptr(),
+                                                col_scale.data_ptr() if col_scale is not None else None,
+                                                bias.data_ptr() if bias is not None else None, y.data_ptr(), M, N, K,
+                                                splits, flags, stream)
+            _check(rc, "w4a16_gemm_noalloc")
+            return y
         nbytes = lib.qlinear_w4a16_workspace_bytes(xdt, M, N, K, splits, flags, x.device.index)
         ws = _workspaces.get(x.device, stream, nbytes) if nbytes else None
         rc = lib.qlinear_w4a16_gemm(xdt, _DTYPE_CODE[out_dtype], x.data_ptr(),

@@ -241,34 +241,9 @@ int check_w4a16_shape(int64_t M, int64_t N, int64_t K) {
   return QL_OK;
 }
 
-}  // namespace
-
-extern "C" {
-
-const char* qlinear_last_error(void) { return g_last_error.c_str(); }
-
-int qlinear_abi_version(void) { return (2 << 16) | 0; }
-
-size_t qlinear_w4a16_workspace_bytes(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, int flags,
-                                     int device) {
-  if (check_w4a16_shape(M, N, K) != QL_OK || M == 0) return 0;
-  int cus = 0;
-  if (device_cus(device, &cus) != QL_OK) return 0;
-  return plan_w4a16(x_dtype, M, N, K, splits, flags, cus).total;
-}
-
-int qlinear_w4a16_auto_splits(int64_t M, int64_t N, int64_t K, int device) {
-  if (int rc = check_w4a16_shape(M, N, K)) return -rc;
-  int cus = 0;
-  if (int rc = device_cus(device, &cus)) return -rc;
-  if (M == 0) return 1;
-  const W4A16Plan pl = plan_w4a16(QL_F16, M, N, K, 0, 0, cus);
-  return pl.dp_tiles < pl.tiles_m * pl.tiles_n ? pl.ksplit : 1;
-}
-
-int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const float* row_scale, const void* w_q4,
-                       const float* w_scale, const float* col_scale, const void* bias, void* y, int64_t M, int64_t N,
-                       int64_t K, int splits, int flags, void* workspace, size_t workspace_bytes, void* stream) {
+// Argument checks of qlinear_w4a16_gemm that need no device: dtypes, shape, splits, flags.
+int check_w4a16_args(int x_dtype, int out_dtype, const float* row_scale, int64_t M, int64_t N, int64_t K, int splits,
+                     int flags) {
   if (x_dtype != QL_BF16 && x_dtype != QL_F16 && x_dtype != QL_F32)
     return fail(QL_ERR_DTYPE, "x dtype %s (%d) unsupported, expected bfloat16, float16 or float32", dtype_name(x_dtype),
                 x_dtype);
@@ -303,6 +278,66 @@ int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const float* r
   if (row_scale && x_dtype != QL_F16)
     return fail(QL_ERR_ARG, "row_scale is only accepted with float16 x (from qlinear_rows_to_f16), got %s",
                 dtype_name(x_dtype));
+  return QL_OK;
+}
+
+// ---- static scratch of the allocation-free W4A16 entry point ---------------------------------
+// qlinear_w4a16_gemm_noalloc runs the same plan as qlinear_w4a16_gemm with this array as its
+// workspace. Every GPU the library runs on holds its own copy (its code object's, loaded with the
+// library) until the process ends. In host code `scratch` only names the symbol: its device
+// address comes from hipGetSymbolAddress, once per device, with that device current, and only
+// that address is passed to kernels.
+constexpr size_t kNoAllocScratchBytes = QL_W4A16_NOALLOC_SCRATCH_BYTES;
+__device__ __attribute__((aligned(256))) uint8_t scratch[kNoAllocScratchBytes];
+
+int scratch_address(void** out) {
+  static std::mutex mu;
+  static void* addr[256] = {nullptr};
+  int device = 0;
+  if (hipGetDevice(&device) != hipSuccess) return fail(QL_ERR_DEVICE, "hipGetDevice failed");
+  if (device < 0 || device >= 256) return fail(QL_ERR_DEVICE, "device index %d out of range", device);
+  std::lock_guard<std::mutex> lock(mu);
+  if (!addr[device]) {
+    void* p = nullptr;
+    const hipError_t e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(QL_ERR_DEVICE, "hipGetSymbolAddress(scratch) on device %d: %s", device, hipGetErrorString(e));
+    addr[device] = p;
+  }
+  *out = addr[device];
+  return QL_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* qlinear_last_error(void) { return g_last_error.c_str(); }
+
+int qlinear_abi_version(void) { return (2 << 16) | 0; }
+
+size_t qlinear_w4a16_workspace_bytes(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, int flags,
+                                     int device) {
+  // invalid arguments (a forced configuration that does not exist among them) plan nothing
+  if (check_w4a16_args(x_dtype, QL_F32, nullptr, M, N, K, splits, flags) != QL_OK || M == 0) return 0;
+  int cus = 0;
+  if (device_cus(device, &cus) != QL_OK) return 0;
+  return plan_w4a16(x_dtype, M, N, K, splits, flags, cus).total;
+}
+
+int qlinear_w4a16_auto_splits(int64_t M, int64_t N, int64_t K, int device) {
+  if (int rc = check_w4a16_shape(M, N, K)) return -rc;
+  int cus = 0;
+  if (int rc = device_cus(device, &cus)) return -rc;
+  if (M == 0) return 1;
+  const W4A16Plan pl = plan_w4a16(QL_F16, M, N, K, 0, 0, cus);
+  return pl.dp_tiles < pl.tiles_m * pl.tiles_n ? pl.ksplit : 1;
+}
+
+int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const float* row_scale, const void* w_q4,
+                       const float* w_scale, const float* col_scale, const void* bias, void* y, int64_t M, int64_t N,
+                       int64_t K, int splits, int flags, void* workspace, size_t workspace_bytes, void* stream) {
+  if (int rc = check_w4a16_args(x_dtype, out_dtype, row_scale, M, N, K, splits, flags)) return rc;
   if (M == 0) return ok();
   if (!x || !w_q4 || !w_scale || !y) return fail(QL_ERR_ARG, "null x / w_q4 / w_scale / y pointer");
   if (!aligned16(x) || !aligned16(w_q4))
@@ -362,6 +397,28 @@ int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const float* r
                            : w4a16_launch(pl.cfg, bf16_mfma, p, (hipStream_t)stream);
   if (e != hipSuccess) return fail(QL_ERR_LAUNCH, "w4a16 launch failed: %s", hipGetErrorString(e));
   return ok();
+}
+
+int qlinear_w4a16_gemm_noalloc(int x_dtype, int out_dtype, const void* x, const float* row_scale, const void* w_q4,
+                               const float* w_scale, const float* col_scale, const void* bias, void* y, int64_t M,
+                               int64_t N, int64_t K, int splits, int flags, void* stream) {
+  // the checks qlinear_w4a16_gemm makes before planning, so the size check below sees a valid plan
+  if (int rc = check_w4a16_args(x_dtype, out_dtype, row_scale, M, N, K, splits, flags)) return rc;
+  if (M == 0) return ok();
+  int cus = 0;
+  if (int rc = device_cus(-1, &cus)) return rc;
+  const size_t need = plan_w4a16(x_dtype, M, N, K, splits, flags, cus).total;
+  if (need > kNoAllocScratchBytes)
+    return fail(QL_ERR_WORKSPACE,
+                "qlinear_w4a16_gemm_noalloc: this call needs %zu bytes of scratch (M=%lld N=%lld K=%lld splits=%d "
+                "flags=%d), more than the %zu bytes of the static scratch; use qlinear_w4a16_gemm with a workspace",
+                need, (long long)M, (long long)N, (long long)K, splits, flags, kNoAllocScratchBytes);
+  void* ws = nullptr;
+  if (need > 0) {
+    if (int rc = scratch_address(&ws)) return rc;
+  }
+  return qlinear_w4a16_gemm(x_dtype, out_dtype, x, row_scale, w_q4, w_scale, col_scale, bias, y, M, N, K, splits,
+                            flags, ws, need > 0 ? kNoAllocScratchBytes : 0, stream);
 }
 
 int qlinear_w4a16_col_scales(const float* w_scale, float* col_scale, int64_t N, int64_t K, void* stream) {

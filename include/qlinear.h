@@ -100,6 +100,22 @@ int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const float* r
                        const void* bias, void* y, int64_t M, int64_t N, int64_t K, int splits,
                        int flags, void* workspace, size_t workspace_bytes, void* stream);
 
+/* Allocation-free variant of qlinear_w4a16_gemm, with the same arguments, checks and results
+ * minus the workspace. No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (code under HIP graph capture, tight serving loops, harnesses that forbid it).
+ * Its workspace is a static device array of QL_W4A16_NOALLOC_SCRATCH_BYTES in the library, one
+ * per GPU, held from the library's load until the process ends; the call makes no hipMalloc,
+ * hipFree or other allocation. A call whose plan needs more scratch than that (see
+ * qlinear_w4a16_workspace_bytes) fails with QL_ERR_WORKSPACE before launching anything. Every
+ * call on one GPU shares that GPU's array: calls that overlap on one GPU (different streams or
+ * host threads without ordering) race on it; calls on one stream are ordered. The scratch needs
+ * no initial contents (each call writes what it reads). */
+#define QL_W4A16_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+int qlinear_w4a16_gemm_noalloc(int x_dtype, int out_dtype, const void* x, const float* row_scale,
+                               const void* w_q4, const float* w_scale, const float* col_scale,
+                               const void* bias, void* y, int64_t M, int64_t N, int64_t K,
+                               int splits, int flags, void* stream);
+
 /* Column factors of the fp16 dequant: col_scale[n] = 2^e_n with 8 * max_g |w_scale[n, g]| * 2^-e_n
  * in [2^14, 2^15) (e_n clamped to [-126, 126]; 1 for a column whose scales are all 0 or not
  * finite). The tile kernels (configurations 0-6 on the fp16 route) dequantize column n as
