@@ -61,7 +61,9 @@ SIGNATURES = {
     "qlinear_qk_norm_rope": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64,
                                       _c_i64, _c_i64, _c_i64, ctypes.c_float, _c_vp]),
     "qlinear_w4a4_gemm": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int,
-                                   _c_vp]),
+                                   _c_int, _c_vp, _c_size_t, _c_vp]),
+    "qlinear_w4a4_auto_splits": (_c_int, [_c_i64, _c_i64, _c_i64, _c_int]),
+    "qlinear_w4a4_workspace_bytes": (_c_size_t, [_c_i64, _c_i64, _c_i64, _c_int, _c_int]),
     "qlinear_rotate_rows_to_f16": (_c_int, [_c_int, _c_vp, _c_vp, _c_int, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
     "qlinear_heads_to_f16": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp,
                                       _c_vp, _c_vp]),
@@ -453,11 +455,22 @@ def rotate_rows_to_f16(x: torch.Tensor, signs: torch.Tensor, group: int) -> tupl
     return x16, rs
 
 
+def w4a4_auto_splits(M: int, N: int, K: int, device: torch.device | int | None = None) -> int:
+    """The split-K count splits=0 resolves to in w4a4_gemm (the reference's auto_splits rule)."""
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device("cuda", device) \
+        if isinstance(device, int) else device
+    rc = load_library().qlinear_w4a4_auto_splits(M, N, K, dev.index)
+    if rc < 0:
+        _check(-rc, "w4a4_auto_splits")
+    return rc
+
+
 def w4a4_gemm(a_q4: torch.Tensor, a_scale: torch.Tensor, b_q4: torch.Tensor, b_scale: torch.Tensor,
               bias: torch.Tensor | None = None, out_dtype: torch.dtype = torch.float32,
-              qblock: int = 32) -> torch.Tensor:
+              qblock: int = 32, splits: int = 1) -> torch.Tensor:
     """y[M, N] from block-scaled int4 activations (quantize_int4) and int4 weights with the
-    reference's per-block fmaf accumulation in K order (see include/qlinear.h)."""
+    reference's per-block fmaf accumulation in K order and, for splits > 1 (0 = the reference's
+    automatic choice), its per-split fp32 partials summed in split order (see include/qlinear.h)."""
     lib = load_library()
     a_q4, b_q4 = _dev_tensor(a_q4, "A_packed"), _dev_tensor(b_q4, "B_packed")
     if a_q4.device != b_q4.device:
@@ -484,13 +497,19 @@ def w4a4_gemm(a_q4: torch.Tensor, a_scale: torch.Tensor, b_q4: torch.Tensor, b_s
             raise RuntimeError(f"bias dtype {bias.dtype} != out dtype {out_dtype}")
         if bias.numel() != N:
             raise RuntimeError(f"bias must have {N} elements, got {bias.numel()}")
+    if not 0 <= int(splits) <= 8:
+        raise RuntimeError(f"splits must be in [0, 8], got {splits}")
     y = torch.empty((M, N), dtype=out_dtype, device=a_q4.device)
     if M == 0:
         return y
     with torch.cuda.device(a_q4.device):
+        stream = _stream_ptr(a_q4.device)
+        nbytes = lib.qlinear_w4a4_workspace_bytes(M, N, K, int(splits), a_q4.device.index)
+        ws = _workspaces.get(a_q4.device, stream, nbytes) if nbytes else None
         rc = lib.qlinear_w4a4_gemm(_DTYPE_CODE[out_dtype], a_q4.data_ptr(), a_scale.data_ptr(), b_q4.data_ptr(),
                                    b_scale.data_ptr(), bias.data_ptr() if bias is not None else None, y.data_ptr(),
-                                   M, N, K, qblock, _stream_ptr(a_q4.device))
+                                   M, N, K, qblock, int(splits), ws.data_ptr() if ws is not None else None,
+                                   ws.numel() if ws is not None else 0, stream)
     _check(rc, "w4a4_gemm")
     return y
 

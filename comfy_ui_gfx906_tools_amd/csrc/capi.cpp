@@ -281,6 +281,20 @@ int check_w4a16_args(int x_dtype, int out_dtype, const float* row_scale, int64_t
   return QL_OK;
 }
 
+// The reference's split-K choice for gemm_int4 (csrc/binding.cpp:21-43 of the reference): none
+// when its 64 x 64 tiles fill two workgroups per CU, else about 2.4 rounds of workgroups, at most
+// 8 splits and at least 8 k-tiles (of 128 K) per split.
+constexpr int kW4A4MaxSplits = 8;
+int w4a4_reference_splits(int64_t M, int64_t N, int64_t K, int cus) {
+  const int64_t tiles = ((M + 63) / 64) * ((N + 63) / 64);
+  const int64_t slots = (int64_t)cus * 2;
+  if (tiles >= slots || tiles == 0) return 1;
+  const int64_t k_tiles = (K / 32 + 3) / 4;
+  const int64_t max_splits = std::min<int64_t>(kW4A4MaxSplits, std::max<int64_t>(1, k_tiles / 8));
+  const int64_t wanted = (12 * slots + 5 * tiles - 1) / (5 * tiles);
+  return (int)std::min(wanted, max_splits);
+}
+
 // ---- static scratch of the allocation-free W4A16 entry point ---------------------------------
 // qlinear_w4a16_gemm_noalloc runs the same plan as qlinear_w4a16_gemm with this array as its
 // workspace. Every GPU the library runs on holds its own copy (its code object's, loaded with the
@@ -591,8 +605,28 @@ int qlinear_gated_residual(int dtype, void* out, const void* x, const void* gate
   return ok();
 }
 
+int qlinear_w4a4_auto_splits(int64_t M, int64_t N, int64_t K, int device) {
+  if (M < 0 || N <= 0 || K < 32 || K % 32 != 0 || M > INT32_MAX / 2 || N > INT32_MAX / 2 || K > (1 << 30)) {
+    fail(QL_ERR_SHAPE, "expected M >= 0, N > 0, K %% 32 == 0, K >= 32; got M=%lld N=%lld K=%lld", (long long)M,
+         (long long)N, (long long)K);
+    return -QL_ERR_SHAPE;
+  }
+  int cus = 0;
+  if (int rc = device_cus(device, &cus)) return -rc;
+  return w4a4_reference_splits(M, N, K, cus);
+}
+
+size_t qlinear_w4a4_workspace_bytes(int64_t M, int64_t N, int64_t K, int splits, int device) {
+  if (M <= 0 || N <= 0 || K < 32 || K % 32 != 0 || splits < 0 || splits > kW4A4MaxSplits) return 0;
+  int cus = 0;
+  if (splits == 0 && device_cus(device, &cus) != QL_OK) return 0;
+  const int s = splits == 0 ? w4a4_reference_splits(M, N, K, cus) : splits;
+  return s > 1 ? (size_t)s * (size_t)M * (size_t)N * sizeof(float) : 0;
+}
+
 int qlinear_w4a4_gemm(int out_dtype, const void* a_q4, const float* a_scale, const void* b_q4, const float* b_scale,
-                      const void* bias, void* y, int64_t M, int64_t N, int64_t K, int qblock, void* stream) {
+                      const void* bias, void* y, int64_t M, int64_t N, int64_t K, int qblock, int splits,
+                      void* workspace, size_t workspace_bytes, void* stream) {
   if (out_dtype != QL_F32 && out_dtype != QL_F16 && out_dtype != QL_BF16)
     return fail(QL_ERR_DTYPE, "out dtype %s (%d) unsupported, expected float32/float16/bfloat16", dtype_name(out_dtype),
                 out_dtype);
@@ -602,8 +636,20 @@ int qlinear_w4a4_gemm(int out_dtype, const void* a_q4, const float* a_scale, con
                 "K=%lld", (long long)M, (long long)N, (long long)K);
   const int64_t tiles = ((M + 127) / 128) * ((N + 127) / 128);
   if (tiles > INT32_MAX) return fail(QL_ERR_SHAPE, "too many 128 x 128 tiles (M=%lld N=%lld)", (long long)M, (long long)N);
+  if (splits < 0 || splits > kW4A4MaxSplits)
+    return fail(QL_ERR_ARG, "splits must be in [0, %d], got %d", kW4A4MaxSplits, splits);
   if (M == 0) return ok();
   if (!a_q4 || !a_scale || !b_q4 || !b_scale || !y) return fail(QL_ERR_ARG, "null a_q4 / a_scale / b_q4 / b_scale / y pointer");
+  if (splits == 0) {
+    int cus = 0;
+    if (int rc = device_cus(-1, &cus)) return rc;
+    splits = w4a4_reference_splits(M, N, K, cus);
+  }
+  const size_t need = splits > 1 ? (size_t)splits * (size_t)M * (size_t)N * sizeof(float) : 0;
+  if (need && (!workspace || workspace_bytes < need))
+    return fail(QL_ERR_WORKSPACE, "split-K over %d splits needs a workspace of %zu bytes (fp32 [%d, %lld, %lld]), got "
+                "%zu at %p", splits, need, splits, (long long)M, (long long)N, workspace_bytes, workspace);
+  if (need && ((uintptr_t)workspace & 3u)) return fail(QL_ERR_ALIGN, "workspace must be 4-byte aligned");
   if (!aligned16(a_q4) || !aligned16(b_q4)) return fail(QL_ERR_ALIGN, "a_q4 and b_q4 must be 16-byte aligned");
   if (((uintptr_t)a_scale & 3u) || ((uintptr_t)b_scale & 3u))
     return fail(QL_ERR_ALIGN, "a_scale and b_scale must be 4-byte aligned");
@@ -620,6 +666,11 @@ int qlinear_w4a4_gemm(int out_dtype, const void* a_q4, const float* a_scale, con
   p.out_dtype = out_dtype;
   p.tiles_m = (int)((M + 127) / 128);
   p.tiles_n = (int)((N + 127) / 128);
+  // the reference's k-tiles of 4 blocks of 32 K (128 K) are this kernel's int4 stages
+  const int k_tiles = (int)((K / 32 + 3) / 4);
+  p.splits = splits;
+  p.stages_per_split = (k_tiles + splits - 1) / splits;
+  p.partial = (float*)workspace;
   const hipError_t e = w4a4_launch(qblock, p, (hipStream_t)stream);
   if (e != hipSuccess) return fail(QL_ERR_LAUNCH, "w4a4 launch failed: %s", hipGetErrorString(e));
   return ok();

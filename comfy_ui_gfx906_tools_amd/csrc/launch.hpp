@@ -102,6 +102,10 @@ struct W4A4Params {
   int M, N, K;
   int out_dtype;
   int tiles_m, tiles_n;  // 128 x 128 tiles
+  // split-K (int4 only): splits > 1 cuts K into ranges of stages_per_split 128-K stages; split s
+  // writes its fp32 partial [M, N] (no bias) to partial + s * M * N, summed by a second kernel
+  int splits, stages_per_split;
+  float* partial;
 };
 hipError_t w4a4_launch(int qblock, const W4A4Params& p, hipStream_t stream);
 // The same kernel with int8 codes ([M, K] / [N, K], block-32 scales): the reference's gemm_int8.

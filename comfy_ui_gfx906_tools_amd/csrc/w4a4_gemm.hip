@@ -1,9 +1,13 @@
 // Block-scaled int4 (W4A4) and int8 GEMMs on gfx950 with the reference's numerics (nodes/ComfyUI-Gfx906Int4/csrc/
-// int4_gemm_scaled.hip:53-191, gemm_int4 with splits = 1): A [M, K/2] and B [N, K/2] packed int4
-// (two's-complement nibbles, low nibble first), scales As [M, K/qb], Bs [N, K/qb] fp32, qb = 32 or
-// 16. For every quant block in K order: ip = exact int32 dot of the block's codes, then
+// int4_gemm_scaled.hip:53-191, 229-246): A [M, K/2] and B [N, K/2] packed int4 (two's-complement
+// nibbles, low nibble first), scales As [M, K/qb], Bs [N, K/qb] fp32, qb = 32 or 16. For every
+// quant block in K order: ip = exact int32 dot of the block's codes, then
 // acc = fmaf(float(ip), as * bs, acc); finally y = acc (+ bias) rounded to the output dtype.
-// The result is bit-identical to that sequence.
+// Split-K (splits > 1, int4): K is cut into ranges of stages_per_split 128-K stages (the
+// reference's k-tiles of 4 blocks of 32), each range accumulates from 0 into an fp32 partial, and
+// w4a4_splitk_reduce_kernel forms y = ((0 + p_0) + p_1) + ... (+ bias) in split order, the
+// reference's splitk_reduce_kernel (int4_gemm_scaled.hip:182-191). The result is bit-identical to
+// those sequences.
 //
 // * One quant block of 32 K is exactly the K of v_mfma_i32_16x16x32_i8, so each MFMA yields one
 //   block's integer dot for a 16 x 16 fragment (with qb = 16, two MFMAs per block, each with the
@@ -64,6 +68,9 @@ __global__ __launch_bounds__(256) void w4a4_gemm_kernel(W4A4Params p) {
   const int g = xcd_remap(blockIdx.x, gridDim.x);
   int tm, tn;
   tile_coords(g, p.tiles_m, p.tiles_n, kW4GroupM, tm, tn);
+  // this workgroup's K range in stages: all of K, or split blockIdx.y's share (possibly empty)
+  const int s_first = p.splits > 1 ? (int)blockIdx.y * p.stages_per_split : 0;
+  const int s_end = p.splits > 1 ? min(S, s_first + p.stages_per_split) : S;
   const int m0 = tm * kW4BM, n0 = tn * kW4BN;
   const uint8_t* A = (const uint8_t*)p.a;
   const uint8_t* B = (const uint8_t*)p.b;
@@ -123,12 +130,12 @@ __global__ __launch_bounds__(256) void w4a4_gemm_kernel(W4A4Params p) {
 #pragma unroll
     for (int fn = 0; fn < 4; ++fn) acc[fm][fn] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  load_regs(0);
+  load_regs(s_first);
   store_lds(0);
   __syncthreads();
-  for (int s = 0; s < S; ++s) {
-    const int buf = s & 1;
-    if (s + 1 < S) load_regs(s + 1);
+  for (int s = s_first; s < s_end; ++s) {
+    const int buf = (s - s_first) & 1;
+    if (s + 1 < s_end) load_regs(s + 1);
     u32x4 a_raw[4], b_raw[4];
 #pragma unroll
     for (int f = 0; f < 4; ++f) {
@@ -179,16 +186,21 @@ __global__ __launch_bounds__(256) void w4a4_gemm_kernel(W4A4Params p) {
               acc[fm][fn][e] = __builtin_fmaf((float)part[fm][fn][e], sa[fm][e] * sb[fn], acc[fm][fn][e]);
       }
     }
-    if (s + 1 < S) store_lds(buf ^ 1);
+    if (s + 1 < s_end) store_lds(buf ^ 1);
     __syncthreads();
   }
 
-  // ---- epilogue: y = acc (+ bias), rounded once to the output dtype ----------------------------
+  // ---- epilogue: y = acc (+ bias), rounded once to the output dtype; a split's partial goes out
+  //      as plain fp32 without bias ------------------------------------------------------------
+  const bool split = p.splits > 1;
+  void* dst = split ? (void*)(p.partial + (size_t)blockIdx.y * M * N) : p.y;
+  const int dst_dtype = split ? (int)kF32 : p.out_dtype;
+  const void* bias = split ? nullptr : p.bias;
 #pragma unroll
   for (int fn = 0; fn < 4; ++fn) {
     const int n = n0 + wn * 64 + fn * 16 + r16;
     if (n >= N) continue;
-    const float bv = p.bias ? read_elem(p.bias, p.out_dtype, n) : 0.0f;
+    const float bv = bias ? read_elem(bias, p.out_dtype, n) : 0.0f;
 #pragma unroll
     for (int fm = 0; fm < 4; ++fm)
 #pragma unroll
@@ -196,26 +208,47 @@ __global__ __launch_bounds__(256) void w4a4_gemm_kernel(W4A4Params p) {
         const int m = m0 + wm * 64 + fm * 16 + 4 * j4 + e;
         if (m >= M) continue;
         float v = acc[fm][fn][e];
-        if (p.bias) v = v + bv;
-        write_elem(p.y, p.out_dtype, (size_t)m * N + n, v);
+        if (bias) v = v + bv;
+        write_elem(dst, dst_dtype, (size_t)m * N + n, v);
       }
   }
+}
+
+// y[i] = ((0 + partial[0][i]) + partial[1][i]) + ... (+ bias[i % N]) in fp32, rounded once to the
+// output dtype: the reference's split-K reduction, element by element.
+__global__ __launch_bounds__(256) void w4a4_splitk_reduce_kernel(const float* __restrict__ partial,
+                                                                 const void* __restrict__ bias, void* __restrict__ y,
+                                                                 int out_dtype, int splits, long MN, int N) {
+  const long i = (long)blockIdx.x * 256 + threadIdx.x;
+  if (i >= MN) return;
+  float v = 0.0f;
+  for (int s = 0; s < splits; ++s) v += partial[(size_t)s * MN + i];
+  if (bias) v += read_elem(bias, out_dtype, (size_t)(i % N));
+  write_elem(y, out_dtype, (size_t)i, v);
 }
 
 }  // namespace
 
 hipError_t w4a4_launch(int qblock, const W4A4Params& p, hipStream_t stream) {
-  const dim3 grid((unsigned)(p.tiles_m * p.tiles_n)), block(256);
+  const int splits = p.splits > 1 ? p.splits : 1;
+  const dim3 grid((unsigned)(p.tiles_m * p.tiles_n), (unsigned)splits), block(256);
   if (qblock == 32)
     hipLaunchKernelGGL((w4a4_gemm_kernel<1, false>), grid, block, 0, stream, p);
   else
     hipLaunchKernelGGL((w4a4_gemm_kernel<2, false>), grid, block, 0, stream, p);
+  if (splits > 1) {
+    const long MN = (long)p.M * p.N;
+    hipLaunchKernelGGL(w4a4_splitk_reduce_kernel, dim3((unsigned)((MN + 255) / 256)), dim3(256), 0, stream,
+                       (const float*)p.partial, p.bias, p.y, p.out_dtype, splits, MN, p.N);
+  }
   return hipGetLastError();
 }
 
 hipError_t int8_block32_launch(const W4A4Params& p, hipStream_t stream) {
+  W4A4Params q = p;
+  q.splits = 1;
   const dim3 grid((unsigned)(p.tiles_m * p.tiles_n)), block(256);
-  hipLaunchKernelGGL((w4a4_gemm_kernel<1, true>), grid, block, 0, stream, p);
+  hipLaunchKernelGGL((w4a4_gemm_kernel<1, true>), grid, block, 0, stream, q);
   return hipGetLastError();
 }
 

@@ -7,12 +7,14 @@ binding.cpp:52-112, 359-372: the module `_get_ext()` returns in ops.py:14-34), o
 
 Same argument meaning, shapes and error behaviour (RuntimeError naming expected vs actual), so
 the reference's own `int4_linear` -- ext.quantize_int4 then ext.gemm_int4 (ops.py:181-182), its
-W4A4 production path -- runs unchanged on MI355X with bit-identical results to its unsplit run:
-the activation quantizer follows the reference kernel's rule (scale = amax * (1/7), rint) and the
-GEMM its per-block fmaf order. `splits` is accepted for compatibility; the MI355X kernel never
-cuts K (the reference's split-K adds per-split fp32 partials, another association of the same
-sum), so gemm_int4_auto_splits returns 1. The block-32 int8 functions of the reference extension
-(quantize_int8 / gemm_int8 / conv_int8, used by its VAE and training nodes) are not provided.
+W4A4 production path -- runs unchanged on MI355X with bit-identical results: the activation
+quantizer follows the reference kernel's rule (scale = amax * (1/7), rint), the GEMM its
+per-block fmaf order, and split-K (splits > 1, or splits = 0 resolved by the reference's
+auto_splits rule for this GPU's CU count) its per-split fp32 partials summed in split order.
+Also provided: the block-32 int8 pair quantize_int8 / gemm_int8 (csrc/binding.cpp:173-217,
+bit-identical to its kernel for every tile config) and the engine's own entry points
+w4a16_linear, quantize_int8_per_token and w8a8_linear. The reference's conv_int8 and attention
+functions (VAE, attention nodes) are outside this package.
 """
 from __future__ import annotations
 
@@ -39,12 +41,14 @@ def gemm_int4(A_packed: torch.Tensor, A_scale: torch.Tensor, B_packed: torch.Ten
         raise RuntimeError("inputs must be on device")
     if not 0 <= int(splits) <= MAX_SPLITS:
         raise RuntimeError(f"splits must be in [0, {MAX_SPLITS}], got {splits}")
-    return _lib.w4a4_gemm(A_packed, A_scale, B_packed, B_scale, bias, out_dtype=out_dtype, qblock=int(qblock))
+    return _lib.w4a4_gemm(A_packed, A_scale, B_packed, B_scale, bias, out_dtype=out_dtype, qblock=int(qblock),
+                          splits=int(splits))
 
 
 def gemm_int4_auto_splits(M: int, N: int, K: int) -> int:
-    """Split-K count gemm_int4 uses for [M, K] x [N, K]^T: always 1 here (no K cut)."""
-    return 1
+    """Split-K count gemm_int4 picks for [M, K] x [N, K]^T (the reference's rule, binding.cpp:36-43,
+    with the current GPU's CU count)."""
+    return _lib.w4a4_auto_splits(int(M), int(N), int(K))
 
 
 def quantize_int8(x: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:

@@ -196,14 +196,27 @@ int qlinear_w8a8_gemm(int out_dtype, const int8_t* xq, const float* x_scale, con
  * qlinear_quantize_int4, rule 1) and b_q4 [N, K/2] packed int4, scales a_scale [M, K/qblock],
  * b_scale [N, K/qblock] fp32, qblock 32 or 16. For each quant block in K order:
  *   ip = exact int32 dot of the block's codes; acc = fmaf(float(ip), a_scale * b_scale, acc)
- * then y = acc (+ bias) rounded once to out_dtype (bias of dtype out_dtype): bit-identical to
- * gemm_dispatch (csrc/int4_gemm_scaled.hip:254-269, kernel :53-191) run unsplit (splits = 1;
- * its split-K runs add per-split fp32 partials, a different association). Counterpart of
- * ext.gemm_int4 (csrc/binding.cpp:70-112). K % 32 == 0; a_q4, b_q4 16-byte aligned.
+ * then y = acc (+ bias) rounded once to out_dtype (bias of dtype out_dtype). splits > 1 (at most
+ * 8): K is cut into ranges of ceil(k_tiles / splits) k-tiles of 128 K (k_tiles = ceil(K / 128)),
+ * each range accumulates from 0 into an fp32 partial [M, N] in the workspace, and
+ * y = ((0 + p_0) + p_1) + ... (+ bias) in split order. splits 0 = the reference's automatic
+ * choice (qlinear_w4a4_auto_splits). Bit-identical to gemm_dispatch (csrc/int4_gemm_scaled.hip:
+ * 254-269, kernel :53-191, split-K :182-191, 229-246) with the same splits. Counterpart of
+ * ext.gemm_int4 (csrc/binding.cpp:70-112). workspace: qlinear_w4a4_workspace_bytes(...) bytes
+ * (splits * M * N fp32 when splits > 1, else none). K % 32 == 0; a_q4, b_q4 16-byte aligned.
  * ------------------------------------------------------------------------------------- */
 int qlinear_w4a4_gemm(int out_dtype, const void* a_q4, const float* a_scale, const void* b_q4,
                       const float* b_scale, const void* bias, void* y, int64_t M, int64_t N,
-                      int64_t K, int qblock, void* stream);
+                      int64_t K, int qblock, int splits, void* workspace, size_t workspace_bytes,
+                      void* stream);
+/* The split count splits = 0 resolves to, the reference's auto_splits (csrc/binding.cpp:36-43,
+ * gemm_int4_auto_splits :359-362) with this device's CU count: 1 when ceil(M/64) * ceil(N/64)
+ * tiles fill 2 per CU, else min(ceil(12 * 2 CUs / (5 tiles)), 8, max(1, k_tiles / 8)). A
+ * negative value is -status on bad arguments. */
+int qlinear_w4a4_auto_splits(int64_t M, int64_t N, int64_t K, int device);
+/* Workspace bytes of qlinear_w4a4_gemm for these arguments (0 when no split-K, or on bad
+ * arguments). */
+size_t qlinear_w4a4_workspace_bytes(int64_t M, int64_t N, int64_t K, int splits, int device);
 
 /* ---------------------------------------------------------------------------------------
  * Block-32 int8, the reference's gemm_int8 / quantize_int8 (csrc/int8_gemm.hip:66-252,

@@ -290,9 +290,54 @@ def fmaf32(a: np.ndarray, b: np.ndarray, c: np.ndarray) -> np.ndarray:
 # ---------------------------------------------------------------------------------------------
 # W4A4 (the reference's production numerics): block-32 int4 activations x int4 weights
 # ---------------------------------------------------------------------------------------------
-def gemm_int4_w4a4(a_packed, a_scale, b_packed, b_scale, bias=None, block: int = 32) -> np.ndarray:
+def gemm_int4_w4a4(a_packed, a_scale, b_packed, b_scale, bias=None, block: int = 32, splits: int = 1) -> np.ndarray:
     """int4_gemm_scaled.hip:53-180 (SUB=1): per 32-block int32 dot of the signed nibbles, then
-    acc = fmaf(float(ip), as*bs, acc) in K order, + bias (fp32 result)."""
+    acc = fmaf(float(ip), as*bs, acc) in K order, + bias (fp32 result). splits > 1: the split-K
+    association of gemm_split_k below."""
     a = unpack_int4(a_packed).astype(np.int64)
     b = unpack_int4(b_packed).astype(np.int64)
+    if splits > 1:
+        return gemm_split_k(a, a_scale, b, b_scale, bias, block, splits)
     return gemm_int8_block32(a, a_scale, b, b_scale, bias, block)
+
+
+def gemm_split_k(aq, as_, bq, bs, bias, block: int, splits: int) -> np.ndarray:
+    """The reference's split-K gemm_int4 (int4_gemm_scaled.hip:229-246 launch, :123-129 K range,
+    :182-191 reduce): K is cut into k-tiles of 4 loads of 32 codes (128 K); split s takes k-tiles
+    [s t, min(k_tiles, (s + 1) t)) with t = ceil(k_tiles / splits) (possibly none), accumulates
+    its blocks from 0 in K order exactly as the unsplit kernel, and the partials are summed in
+    fp32 as v = ((0 + p_0) + p_1) + ..., then + bias. Pinned by test_split_k_* (tests/test_oracle.py)."""
+    aq = np.asarray(aq, dtype=np.int64)
+    bq = np.asarray(bq, dtype=np.int64)
+    M, K = aq.shape
+    N = bq.shape[0]
+    k_tiles = (K // 32 + 3) // 4
+    per = (k_tiles + splits - 1) // splits
+    v = np.zeros((M, N), dtype=np.float32)
+    for s in range(splits):
+        k_lo = min(K, s * per * 128)
+        k_hi = min(K, (s + 1) * per * 128)
+        if k_hi > k_lo:
+            sl = slice(k_lo // block, k_hi // block)
+            part = gemm_int8_block32(aq[:, k_lo:k_hi], np.asarray(as_)[:, sl], bq[:, k_lo:k_hi], np.asarray(bs)[:, sl],
+                                     None, block)
+        else:
+            part = np.zeros((M, N), dtype=np.float32)
+        v = (v + part).astype(np.float32)
+    if bias is not None:
+        v = (v + np.asarray(bias, dtype=np.float32)[None, :]).astype(np.float32)
+    return v
+
+
+def reference_auto_splits(M: int, N: int, K: int, cus: int) -> int:
+    """binding.cpp:21-43 auto_splits (gemm_tiles / gemm_k_tiles of int4_gemm_scaled.hip:271-272):
+    64 x 64 tiles; none when they fill 2 workgroups per CU, else ceil(12 slots / (5 tiles)) capped at
+    8 and at k_tiles / 8 (at least 1). Pinned by test_reference_auto_splits (the reference's own sweep
+    notes, binding.cpp:31-35)."""
+    tiles = ((M + 63) // 64) * ((N + 63) // 64)
+    slots = cus * 2
+    if tiles >= slots or tiles == 0:
+        return 1
+    max_splits = min(8, max(1, ((K // 32 + 3) // 4) // 8))
+    wanted = (12 * slots + 5 * tiles - 1) // (5 * tiles)
+    return min(wanted, max_splits)

@@ -14,7 +14,7 @@ from tests.conftest import ROOT
 HEADER = os.path.join(ROOT, "include", "qlinear.h")
 LIB = os.path.join(ROOT, "comfy_ui_gfx906_tools_amd", "libqlinear.so")
 
-QL_OK, QL_ERR_ARG, QL_ERR_SHAPE, QL_ERR_DTYPE, QL_ERR_ALIGN = 0, 1, 2, 3, 4
+QL_OK, QL_ERR_ARG, QL_ERR_SHAPE, QL_ERR_DTYPE, QL_ERR_ALIGN, QL_ERR_WORKSPACE = 0, 1, 2, 3, 4, 5
 
 
 def _header_functions():
@@ -142,13 +142,20 @@ def test_quantizer_and_w8a8_argument_checks(lib):
 def test_w4a4_entry_point_checks_arguments(lib):
     p16 = ctypes.c_void_p(256)
     f = lib.qlinear_w4a4_gemm
-    assert f(3, None, None, None, None, None, None, 4, 64, 64, 32, None) == QL_ERR_DTYPE
-    assert f(0, None, None, None, None, None, None, 4, 64, 64, 8, None) == QL_ERR_ARG
-    assert f(0, None, None, None, None, None, None, 4, 64, 48, 32, None) == QL_ERR_SHAPE
-    assert f(0, None, None, None, None, None, None, 0, 64, 64, 32, None) == QL_OK
-    assert f(0, None, None, None, None, None, None, 4, 64, 64, 32, None) == QL_ERR_ARG
-    assert f(0, ctypes.c_void_p(264), p16, p16, p16, None, p16, 4, 64, 64, 16, None) == QL_ERR_ALIGN
-    assert f(0, p16, ctypes.c_void_p(258), p16, p16, None, p16, 4, 64, 64, 16, None) == QL_ERR_ALIGN
+    assert f(3, None, None, None, None, None, None, 4, 64, 64, 32, 1, None, 0, None) == QL_ERR_DTYPE
+    assert f(0, None, None, None, None, None, None, 4, 64, 64, 8, 1, None, 0, None) == QL_ERR_ARG
+    assert f(0, None, None, None, None, None, None, 4, 64, 48, 32, 1, None, 0, None) == QL_ERR_SHAPE
+    assert f(0, None, None, None, None, None, None, 0, 64, 64, 32, 0, None, 0, None) == QL_OK
+    assert f(0, None, None, None, None, None, None, 4, 64, 64, 32, 1, None, 0, None) == QL_ERR_ARG
+    assert f(0, ctypes.c_void_p(264), p16, p16, p16, None, p16, 4, 64, 64, 16, 1, None, 0, None) == QL_ERR_ALIGN
+    assert f(0, p16, ctypes.c_void_p(258), p16, p16, None, p16, 4, 64, 64, 16, 1, None, 0, None) == QL_ERR_ALIGN
+    # split-K: at most 8 splits (binding.cpp MAX_SPLITS), and a workspace of splits * M * N fp32
+    assert f(0, p16, p16, p16, p16, None, p16, 4, 64, 64, 32, 9, None, 0, None) == QL_ERR_ARG
+    assert "splits" in _err(lib)
+    assert f(0, p16, p16, p16, p16, None, p16, 4, 64, 64, 32, 2, None, 0, None) == QL_ERR_WORKSPACE
+    assert "2048 bytes" in _err(lib)
+    assert lib.qlinear_w4a4_workspace_bytes(4, 64, 64, 2, 0) == 2 * 4 * 64 * 4
+    assert lib.qlinear_w4a4_workspace_bytes(4, 64, 64, 1, 0) == 0
 
 
 def test_int8_block32_entry_points_check_arguments(lib):

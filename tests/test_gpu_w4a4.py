@@ -63,8 +63,32 @@ def test_reference_int4_linear_w4a4_bit_exact(M, K, N):
     wp, ws = orc.quantize_pack_int4(w.numpy(), rule="div")
     y = ops.int4_linear_w4a4(x.to(DEV), torch.from_numpy(wp).to(DEV), torch.from_numpy(ws).to(DEV), bias.to(DEV))
     xp, xs = orc.quantize_pack_int4(x.float().numpy(), rule="recip")
-    ref = torch.from_numpy(orc.gemm_int4_w4a4(xp, xs, wp, ws, bias.float().numpy())).to(torch.bfloat16)
+    # gemm_int4's default splits = 0: the reference's auto_splits for this GPU's CU count
+    cus = torch.cuda.get_device_properties(DEV).multi_processor_count
+    splits = orc.reference_auto_splits(M, N, K, cus)
+    assert ext.gemm_int4_auto_splits(M, N, K) == splits
+    ref = torch.from_numpy(orc.gemm_int4_w4a4(xp, xs, wp, ws, bias.float().numpy(), splits=splits)).to(torch.bfloat16)
     assert y.dtype == torch.bfloat16 and torch.equal(y.cpu(), ref)
+
+
+@pytest.mark.parametrize("M,N,K,splits", [(37, 100, 1024, 2), (130, 257, 640, 3), (1, 64, 32, 8), (64, 96, 3072, 0),
+                                          (200, 130, 4096, 8), (300, 520, 1024, 5)])
+@pytest.mark.parametrize("qblock", [32, 16])
+@pytest.mark.parametrize("out_dtype", [torch.float32, torch.bfloat16])
+def test_w4a4_split_k_bit_exact(M, N, K, splits, qblock, out_dtype):
+    """gemm_int4 with split-K: per-split fp32 partials from 0, summed in split order, + bias -- the
+    reference's association (oracle gemm_split_k), bit for bit; splits = 0 resolves to the
+    reference's auto_splits; K = 32 with 8 splits leaves seven splits empty."""
+    print(f"w4a4 split M={M} N={N} K={K} splits={splits} qblock={qblock} out={out_dtype}", flush=True)
+    ap, sa, bp, sb = _operands(M, N, K, qblock, seed=M + N + K + splits + qblock)
+    bias = np.random.default_rng(3).standard_normal(N).astype(np.float32)
+    bias_t = torch.from_numpy(bias).to(out_dtype)
+    y = ext.gemm_int4(*(torch.from_numpy(t).to(DEV) for t in (ap, sa, bp, sb)), bias_t.to(DEV), out_dtype,
+                      splits=splits, qblock=qblock)
+    eff = splits or orc.reference_auto_splits(M, N, K, torch.cuda.get_device_properties(DEV).multi_processor_count)
+    ref = orc.gemm_split_k(orc.unpack_int4(ap), sa, orc.unpack_int4(bp), sb, bias_t.float().numpy(), qblock, eff)
+    assert torch.equal(y.cpu(), torch.from_numpy(ref).to(out_dtype)), \
+        f"max abs diff {np.abs(y.float().cpu().numpy() - ref).max()}"
 
 
 def test_w4a4_c1_shape_rows_match():

@@ -399,6 +399,78 @@ def test_gemm_int4_w4a4_matches_unpacked_int8_path():
     assert np.allclose(got, deq, rtol=1e-5, atol=1e-5)
 
 
+def test_split_k_bruteforce_fractions():
+    """gemm_split_k against exact rationals on a tiny case whose split boundaries are written out:
+    K = 384 is 3 k-tiles of 128; 2 splits take k-tiles {0, 1} (K 0-255) and {2} (K 256-383), each
+    accumulated from 0 with correctly rounded fmaf, then v = (0 + p0) + p1, + bias, each rounded to
+    fp32. 3 splits take one k-tile each; 4 splits leave the last one empty."""
+    rng = np.random.default_rng(21)
+    M, N, K = 2, 3, 384
+    aq = rng.integers(-8, 8, (M, K))
+    bq = rng.integers(-8, 8, (N, K))
+    as_ = rng.uniform(0.01, 1.0, (M, K // 32)).astype(np.float32)
+    bs = rng.uniform(0.01, 1.0, (N, K // 32)).astype(np.float32)
+    bias = rng.standard_normal(N).astype(np.float32)
+
+    def partial(m, n, k_lo, k_hi):
+        acc = Fraction(0)
+        for kb in range(k_lo // 32, k_hi // 32):
+            ip = sum(int(aq[m, k]) * int(bq[n, k]) for k in range(32 * kb, 32 * kb + 32))
+            sc = _f32_nearest(Fraction(float(as_[m, kb])) * Fraction(float(bs[n, kb])))
+            acc = Fraction(float(_f32_nearest(Fraction(ip) * Fraction(float(sc)) + acc)))
+        return acc
+
+    for splits, ranges in ((2, [(0, 256), (256, 384)]), (3, [(0, 128), (128, 256), (256, 384)]),
+                           (4, [(0, 128), (128, 256), (256, 384), (384, 384)])):
+        got = orc.gemm_split_k(aq, as_, bq, bs, bias, 32, splits)
+        for m in range(M):
+            for n in range(N):
+                v = Fraction(0)
+                for lo, hi in ranges:
+                    v = Fraction(float(_f32_nearest(v + partial(m, n, lo, hi))))
+                v = _f32_nearest(v + Fraction(float(bias[n])))
+                assert got[m, n] == v, (splits, m, n)
+
+
+def test_split_k_is_a_reassociation_of_the_unsplit_sum():
+    """One split is the unsplit kernel; on an exactly representable grid (integer codes, power-of-
+    two scales, small K) every association gives the same fp32 sum, so any split count must equal
+    the unsplit result; on random data the split result stays within a few fp32 ulp of it."""
+    rng = np.random.default_rng(22)
+    M, N, K = 5, 7, 1280
+    ap, bp = (((c[:, 0::2] & 0xF) | ((c[:, 1::2] & 0xF) << 4)).astype(np.uint8).view(np.int8)
+              for c in (rng.integers(-8, 8, (M, K)), rng.integers(-8, 8, (N, K))))
+    s2a = (2.0 ** rng.integers(-6, 0, (M, K // 32))).astype(np.float32)
+    s2b = (2.0 ** rng.integers(-6, 0, (N, K // 32))).astype(np.float32)
+    ref = orc.gemm_int4_w4a4(ap, s2a, bp, s2b)
+    for splits in (1, 2, 3, 7, 8):
+        assert np.array_equal(orc.gemm_int4_w4a4(ap, s2a, bp, s2b, splits=splits), ref), splits
+    ra = rng.uniform(0.01, 1.0, (M, K // 32)).astype(np.float32)
+    rb = rng.uniform(0.01, 1.0, (N, K // 32)).astype(np.float32)
+    ref = orc.gemm_int4_w4a4(ap, ra, bp, rb).astype(np.float64)
+    got = orc.gemm_int4_w4a4(ap, ra, bp, rb, splits=4).astype(np.float64)
+    assert np.abs(got - ref).max() <= 8 * np.spacing(np.abs(ref).max().astype(np.float32))
+    assert not np.array_equal(got, ref)  # the association does differ somewhere on random data
+    # qblock 16: two scales per 32-K load, same k-tile boundaries
+    sa16 = rng.uniform(0.01, 1.0, (M, K // 16)).astype(np.float32)
+    sb16 = rng.uniform(0.01, 1.0, (N, K // 16)).astype(np.float32)
+    r16 = orc.gemm_int4_w4a4(ap, sa16, bp, sb16, block=16).astype(np.float64)
+    g16 = orc.gemm_int4_w4a4(ap, sa16, bp, sb16, block=16, splits=3).astype(np.float64)
+    assert np.abs(g16 - r16).max() <= 8 * np.spacing(np.abs(r16).max().astype(np.float32))
+
+
+def test_reference_auto_splits():
+    """The reference's split choice, checked against its own sweep notes (binding.cpp:31-35, on a
+    60-CU gfx906: 4-5 splits best for M=192 N=1536 = 72 tiles, 3 for 96 tiles) and its guards: no
+    split once the 64 x 64 tiles fill 2 per CU, none when K has fewer than 16 k-tiles of 128."""
+    assert orc.reference_auto_splits(192, 1536, 6144, 60) == 4
+    assert orc.reference_auto_splits(256, 1536, 6144, 60) == 3      # 96 tiles
+    assert orc.reference_auto_splits(4608, 3072, 3072, 60) == 1     # fills the GPU
+    assert orc.reference_auto_splits(192, 1536, 1024, 60) == 1      # 8 k-tiles: too short to split
+    assert orc.reference_auto_splits(64, 96, 3072, 256) == 3        # 24 k-tiles: at most 3
+    assert orc.reference_auto_splits(1, 64, 16384, 256) == 8        # capped at 8
+
+
 # ---- committed fixtures --------------------------------------------------------------------------
 def test_golden_w4a16_small():
     f = np.load(golden_path("w4a16_small.npz"))
