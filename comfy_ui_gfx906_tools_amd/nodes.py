@@ -20,6 +20,7 @@ import sys
 
 import torch
 
+from . import _lib
 from .ops import (BLOCK, Gfx906Int4Ops, apply_group_rotation, choose_rotation_group, get_group_rotation,
                   make_load_quantizing_ops, quantize_pack_int4, repack_q4_0_native)
 
@@ -102,11 +103,11 @@ def _float_weight(w) -> tuple[torch.Tensor, str]:
     return w.detach().float(), "plain"
 
 
-def quantize_module_weight(module, block_size: int = BLOCK, rotation_group: int = 0):
+def quantize_module_weight(module, block_size: int = BLOCK, rotation_group: int = 0, rule: int | None = None):
     """(weight_q4 int8 [N, K/2], weight_scale fp32 [N, K/32], source tag) for a Linear-like
     object (nodes.py:157-223): a GGUF Q4_0 weight is repacked losslessly (unless a rotation must
     be folded in); any other format is decoded to fp32, optionally rotated, and quantized by
-    quantize_pack_int4 (the HIP quantizer for device tensors)."""
+    quantize_pack_int4 (the HIP quantizer for device tensors; `rule` as there)."""
     if block_size != BLOCK:
         raise ValueError(f"the packed layout has groups of {BLOCK}, got block_size={block_size}")
     w = module.weight
@@ -120,7 +121,7 @@ def quantize_module_weight(module, block_size: int = BLOCK, rotation_group: int 
         R = get_group_rotation(module.in_features, rotation_group, w_float.device)
         w_float = apply_group_rotation(w_float, R, rotation_group)
         tag += "_rotated"
-    packed, scale = quantize_pack_int4(w_float, block_size)
+    packed, scale = quantize_pack_int4(w_float, block_size, rule)
     return packed, scale, tag
 
 
@@ -186,7 +187,11 @@ def quantize_state_dict(sd: dict, device, metadata: dict | None = None, prefix: 
     (quantized on `device`, stored on the CPU); ConvRot W4A4 layers (named by the metadata, or any
     int8 2-D weight with an fp32 per-row `.weight_scale` sidecar once the file has ConvRot layers)
     are decoded by `convrot_decoder` (comfy_kitchen's dequantize_convrot_w4a4_weight when None)
-    first; every other tensor passes through. Returns (quantized state dict, counts)."""
+    first; every other tensor passes through. Returns (quantized state dict, counts).
+    The reference quantizes a plain float weight where the state dict holds it (the CPU, after
+    load_torch_file: torch's `amax / 7.0` there is a true division) and a decoded ConvRot weight on
+    `device` (torch's GPU rule, amax * fl(1/7)); the same rules are used here, whichever device
+    computes, so the packed weights equal the reference's bit for bit."""
     device = torch.device(device)
     layers = parse_convrot_layers(metadata, prefix)
     shared_cfg = next(iter(layers.values()), None)
@@ -208,6 +213,7 @@ def quantize_state_dict(sd: dict, device, metadata: dict | None = None, prefix: 
         if key in sidecars:
             continue
         base = key[:-len(".weight")] if key.endswith(".weight") else None
+        rule = None  # the rule of the device the weight is quantized on
         if base is not None and base in convrot:
             if convrot_decoder is None:
                 try:
@@ -223,12 +229,14 @@ def quantize_state_dict(sd: dict, device, metadata: dict | None = None, prefix: 
         elif base is not None and t.ndim == 2 and t.shape[1] % block_size == 0 and t.shape[1] >= block_size:
             plain = getattr(t, "tensor_type", None) is None and t.is_floating_point()
             src = RawWeight(t.to(device) if plain else t, t.shape[0], t.shape[1])
+            if plain:  # computed on `device`, with the rule of the device the tensor was loaded on
+                rule = _lib.RULE_RECIP if t.device.type == "cuda" else _lib.RULE_DIV
             counts["quantized"] += 1
         else:
             out[key] = t
             counts["passthrough"] += 1
             continue
-        packed, scale, _ = quantize_module_weight(src, block_size)
+        packed, scale, _ = quantize_module_weight(src, block_size, rule=rule)
         out[base + ".weight_q4"] = packed.cpu()
         out[base + ".weight_scale"] = scale.cpu()
     return out, counts

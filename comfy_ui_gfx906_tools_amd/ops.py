@@ -109,20 +109,23 @@ def apply_group_rotation(t: torch.Tensor, R: torch.Tensor, group: int) -> torch.
 # ---------------------------------------------------------------------------------------------
 # Weight format
 # ---------------------------------------------------------------------------------------------
-def quantize_pack_int4(t: torch.Tensor, block: int = BLOCK):
+def quantize_pack_int4(t: torch.Tensor, block: int = BLOCK, rule: int | None = None):
     """t [..., K] float -> (packed int8 [..., K/2], scale fp32 [..., K/block]) (ops.py:108-126).
     Device tensors are quantized by the HIP kernel with the scale rule torch itself uses on that
     device, so results equal the reference's torch expression on the same device; CPU tensors use
-    that torch expression directly (load-time code, not the forward path)."""
+    that torch expression directly (load-time code, not the forward path). `rule` (_lib.RULE_DIV /
+    RULE_RECIP) overrides the device's rule: a weight the reference would quantize on the CPU can
+    then be quantized on the GPU with the CPU's result."""
     K = t.shape[-1]
     if K % block != 0:
         raise AssertionError(f"last dim {K} not divisible by block {block}")
+    rule = _TORCH_RULE["cuda" if t.device.type == "cuda" else "cpu"] if rule is None else rule
     if t.device.type == "cuda" and block == BLOCK and t.dtype in (torch.float32, torch.float16, torch.bfloat16):
-        return _lib.quantize_int4(t, _TORCH_RULE["cuda"])
+        return _lib.quantize_int4(t, rule)
     shape = t.shape
     tb = t.reshape(-1, K // block, block).float()
     amax = tb.abs().amax(dim=-1, keepdim=True).clamp_min(1e-8)
-    scale = amax / 7.0
+    scale = amax / 7.0 if rule == _lib.RULE_DIV else amax * torch.tensor(1.0 / 7.0, dtype=torch.float32)
     codes = torch.round(tb / scale).clamp(-8, 7).to(torch.int32).reshape(-1, K)
     packed = ((codes[:, 0::2] & 0xF) | ((codes[:, 1::2] & 0xF) << 4)).to(torch.uint8).view(torch.int8)
     return (packed.reshape(*shape[:-1], K // 2).contiguous(),

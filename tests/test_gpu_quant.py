@@ -95,3 +95,26 @@ def test_repack_q4_0_through_ops_on_device():
     p_cpu, s_cpu = ops.repack_q4_0_native(t, out_f, in_f)
     p_dev, s_dev = ops.repack_q4_0_native(t.to(DEV), out_f, in_f)
     assert p_dev.is_cuda and torch.equal(p_dev.cpu(), p_cpu) and torch.equal(s_dev.cpu(), s_cpu)
+
+
+def test_unet_loader_quantizes_cpu_loaded_weights_with_the_cpu_rule():
+    """The reference's UNet loader quantizes a plain float weight where load_torch_file put it, the
+    CPU (nodes.py:557-561 -> quantize_pack_int4 on a CPU tensor: a true `amax / 7.0`). The engine's
+    loader computes on the GPU but must produce the same bytes: nodes.quantize_state_dict(sd, cuda)
+    against the reference's torch expression on the CPU tensors, bit for bit (the GPU's own rule
+    differs from it in the last bit of about half the scales on random data)."""
+    from comfy_ui_gfx906_tools_amd import nodes
+    g = torch.Generator().manual_seed(31)
+    sd = {"a.weight": torch.randn(300, 1024, generator=g) * 0.02,
+          "b.weight": (torch.randn(64, 3072, generator=g) * 0.05).to(torch.bfloat16),
+          "c.weight": (torch.randn(40, 96, generator=g) * 3.0).to(torch.float16)}
+    q, counts = nodes.quantize_state_dict(sd, DEV)
+    assert counts["quantized"] == 3
+    for base in ("a", "b", "c"):
+        p_ref, s_ref = _reference_torch_expression(sd[base + ".weight"])
+        assert q[base + ".weight_q4"].device.type == "cpu"
+        assert torch.equal(q[base + ".weight_scale"], s_ref), base
+        assert torch.equal(q[base + ".weight_q4"], p_ref), base
+    # the GPU rule on the same data does differ somewhere (so the test distinguishes the rules)
+    _, s_gpu = _lib().quantize_int4(sd["a.weight"].to(DEV), 1)
+    assert not torch.equal(s_gpu.cpu(), q["a.weight_scale"])
