@@ -63,6 +63,7 @@ SIGNATURES = {
     "qlinear_w4a4_gemm": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int,
                                    _c_int, _c_vp, _c_size_t, _c_vp]),
     "qlinear_w4a4_auto_splits": (_c_int, [_c_i64, _c_i64, _c_i64, _c_int]),
+    "qlinear_check_launch_plan": (_c_int, [_c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int]),
     "qlinear_w4a4_workspace_bytes": (_c_size_t, [_c_i64, _c_i64, _c_i64, _c_int, _c_int]),
     "qlinear_rotate_rows_to_f16": (_c_int, [_c_int, _c_vp, _c_vp, _c_int, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
     "qlinear_heads_to_f16": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp,

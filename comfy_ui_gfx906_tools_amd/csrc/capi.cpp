@@ -10,7 +10,10 @@
 #include <mutex>
 #include <string>
 
+#include <vector>
+
 #include "../../include/qlinear.h"
+#include "common.hpp"
 #include "launch.hpp"
 
 using namespace qlinear;
@@ -433,6 +436,130 @@ int qlinear_w4a16_gemm_noalloc(int x_dtype, int out_dtype, const void* x, const 
   }
   return qlinear_w4a16_gemm(x_dtype, out_dtype, x, row_scale, w_q4, w_scale, col_scale, bias, y, M, N, K, splits,
                             flags, ws, need > 0 ? kNoAllocScratchBytes : 0, stream);
+}
+
+int qlinear_check_launch_plan(int op, int x_dtype, int64_t M, int64_t N, int64_t K, int splits, int flags, int cus) {
+  if (cus <= 0 || cus > 4096) return fail(QL_ERR_ARG, "cus must be in [1, 4096], got %d", cus);
+  if (M <= 0) return fail(QL_ERR_ARG, "M must be > 0 for a plan check, got %lld", (long long)M);
+  // One launch of `grid` workgroups: workgroup b runs tile (base + xcd_remap(b) / sub) of the
+  // grouped order (rows m0 = tm * tile_rows + (g % sub) * (tile_rows / sub)), K piece g % pieces
+  // (pieces > 1 only for cut tiles). Every (tile, piece, sub) must be covered exactly once over all
+  // launches, every tile must start inside M and N, and a sub-tile that starts past M must be one
+  // the kernel leaves by its early exit (allow_past_m).
+  std::vector<int> seen;
+  int tiles_m = 0, tiles_n = 0;
+  auto fresh = [&](int tm_count, int tn_count, int per_tile) {
+    tiles_m = tm_count;
+    tiles_n = tn_count;
+    seen.assign((size_t)tm_count * tn_count * per_tile, 0);
+  };
+  auto launch = [&](const char* what, int grid, int base, int sub, int pieces, int tile_rows, int tile_cols,
+                    int group_m, bool allow_past_m) -> int {
+    for (int b = 0; b < grid; ++b) {
+      const int g = xcd_remap(b, grid);
+      if (g < 0 || g >= grid)
+        return fail(QL_ERR_SHAPE, "%s: xcd_remap(%d, %d) = %d is not a workgroup of the grid", what, b, grid, g);
+      const int t = base + g / (sub * pieces);
+      const int rest = g % (sub * pieces);
+      if (t < 0 || t >= tiles_m * tiles_n)
+        return fail(QL_ERR_SHAPE, "%s: workgroup %d maps to tile %d of %d", what, b, t, tiles_m * tiles_n);
+      int tm = 0, tn = 0;
+      tile_coords(t, tiles_m, tiles_n, group_m, tm, tn);
+      if (tm < 0 || tm >= tiles_m || tn < 0 || tn >= tiles_n)
+        return fail(QL_ERR_SHAPE, "%s: tile %d -> (%d, %d) outside %d x %d tiles", what, t, tm, tn, tiles_m, tiles_n);
+      const int64_t m0 = (int64_t)tm * tile_rows + (int64_t)(rest % sub) * (tile_rows / sub);
+      const int64_t n0 = (int64_t)tn * tile_cols;
+      if (n0 >= N) return fail(QL_ERR_SHAPE, "%s: workgroup %d starts at column %lld >= N=%lld", what, b, (long long)n0,
+                               (long long)N);
+      if (m0 >= M && !allow_past_m)
+        return fail(QL_ERR_SHAPE, "%s: workgroup %d starts at row %lld >= M=%lld", what, b, (long long)m0, (long long)M);
+      const size_t slot = ((size_t)tm * tiles_n + tn) * (size_t)(sub * pieces) + (size_t)rest;
+      if (slot >= seen.size() || seen[slot]++)
+        return fail(QL_ERR_SHAPE, "%s: tile (%d, %d) part %d launched twice", what, tm, tn, rest);
+    }
+    return QL_OK;
+  };
+  auto all_seen = [&](const char* what) -> int {
+    for (size_t i = 0; i < seen.size(); ++i)
+      if (seen[i] != 1) return fail(QL_ERR_SHAPE, "%s: tile part %zu launched %d times", what, i, seen[i]);
+    return QL_OK;
+  };
+  if (op == 0) {  // W4A16 (qlinear_w4a16_gemm's plan)
+    if (int rc = check_w4a16_args(x_dtype, QL_F32, nullptr, M, N, K, splits, flags)) return rc;
+    const W4A16Plan pl = plan_w4a16(x_dtype, M, N, K, splits, flags, cus);
+    const int tiles = pl.tiles_m * pl.tiles_n;
+    if (pl.cfg == kCfgGemv || pl.cfg == kCfgSkinny) {
+      // column blocks per workgroup, no tiles along M (the direct kernels index columns only)
+      if (pl.BM < M) return fail(QL_ERR_SHAPE, "direct kernel: %d rows per workgroup < M=%lld", pl.BM, (long long)M);
+      return QL_OK;
+    }
+    if (pl.dp_tiles < 0 || pl.dp_tiles > tiles) return fail(QL_ERR_SHAPE, "dp_tiles %d of %d", pl.dp_tiles, tiles);
+    if (is_tile256(pl.cfg)) {
+      // whole 256 x 256 tiles, then the rest as 128-row halves (a half wholly past M exits early)
+      fresh(pl.tiles_m, pl.tiles_n, 2);
+      // whole tiles occupy both halves of their slot
+      for (int b = 0; b < pl.dp_tiles; ++b) {
+        const int g = xcd_remap(b, pl.dp_tiles);
+        int tm = 0, tn = 0;
+        tile_coords(g, tiles_m, tiles_n, kTile256GroupM, tm, tn);
+        if ((int64_t)tm * 256 >= M || (int64_t)tn * 256 >= N)
+          return fail(QL_ERR_SHAPE, "tile256 whole: workgroup %d at (%d, %d) starts outside M x N", b, tm, tn);
+        const size_t slot = ((size_t)tm * tiles_n + tn) * 2;
+        if (seen[slot]++ || seen[slot + 1]++) return fail(QL_ERR_SHAPE, "tile256 whole: tile (%d, %d) twice", tm, tn);
+      }
+      if (int rc = launch("tile256 halves", 2 * (tiles - pl.dp_tiles), pl.dp_tiles, 2, 1, 256, 256, kTile256GroupM, true))
+        return rc;
+      return all_seen("tile256");
+    }
+    // configurations 0-3: whole tiles, then the cut tiles as ksplit K pieces each
+    fresh(pl.tiles_m, pl.tiles_n, 1);
+    if (int rc = launch("w4a16 whole", pl.dp_tiles, 0, 1, 1, pl.BM, pl.BN, kW4A16GroupM, false)) return rc;
+    if (pl.dp_tiles < tiles) {
+      if (pl.ksplit < 1 || pl.ksplit > pl.stages)
+        return fail(QL_ERR_SHAPE, "ksplit %d outside [1, %d stages]", pl.ksplit, pl.stages);
+      std::vector<int> whole = seen;
+      seen.assign((size_t)tiles * pl.ksplit, 0);
+      for (int i = 0; i < tiles; ++i)  // a whole tile stands for all its pieces
+        for (int q = 0; q < pl.ksplit; ++q) seen[(size_t)i * pl.ksplit + q] = whole[i];
+      // the cut launch numbers its pieces tile-major: piece = g - (t - dp) * ksplit
+      for (int b = 0; b < (tiles - pl.dp_tiles) * pl.ksplit; ++b) {
+        const int g = xcd_remap(b, (tiles - pl.dp_tiles) * pl.ksplit);
+        const int t = pl.dp_tiles + g / pl.ksplit, piece = g % pl.ksplit;
+        int tm = 0, tn = 0;
+        tile_coords(t, tiles_m, tiles_n, kW4A16GroupM, tm, tn);
+        if ((int64_t)tm * pl.BM >= M || (int64_t)tn * pl.BN >= N || t >= tiles)
+          return fail(QL_ERR_SHAPE, "w4a16 cut: workgroup %d at tile %d (%d, %d) starts outside M x N", b, t, tm, tn);
+        const int s0 = (int)((long long)piece * pl.stages / pl.ksplit), s1 = (int)((long long)(piece + 1) * pl.stages / pl.ksplit);
+        if (s0 < 0 || s1 < s0 || s1 > pl.stages) return fail(QL_ERR_SHAPE, "w4a16 cut: piece %d range [%d, %d)", piece, s0, s1);
+        const size_t slot = ((size_t)tm * tiles_n + tn) * pl.ksplit + piece;
+        if (seen[slot]++) return fail(QL_ERR_SHAPE, "w4a16 cut: tile (%d, %d) piece %d twice", tm, tn, piece);
+      }
+      const size_t partial_slots = pl.total >= pl.off_partial ? (pl.total - pl.off_partial) / ((size_t)pl.BM * pl.BN * 4) : 0;
+      if (partial_slots < (size_t)(tiles - pl.dp_tiles) * pl.ksplit)
+        return fail(QL_ERR_SHAPE, "w4a16 cut: workspace holds %zu partial tiles, the launch writes %d", partial_slots,
+                    (tiles - pl.dp_tiles) * pl.ksplit);
+    }
+    return all_seen("w4a16");
+  }
+  if (op == 1) {  // W8A8 (qlinear_w8a8_gemm's choice)
+    if (K < 64 || K % 64 != 0 || N <= 0) return fail(QL_ERR_SHAPE, "W8A8 needs K %% 64 == 0, N > 0");
+    const bool big = M > 128 && K * kW8A8Tile256 <= INT32_MAX;
+    const int cfg = M <= 16 ? 3 : M <= 64 ? 2 : 1;
+    const int BM = big ? kW8A8Tile256 : w8a8_config(cfg).BM, BN = big ? kW8A8Tile256 : w8a8_config(cfg).BN;
+    fresh((int)((M + BM - 1) / BM), (int)((N + BN - 1) / BN), 1);
+    if (int rc = launch("w8a8", tiles_m * tiles_n, 0, 1, 1, BM, BN, big ? kW8A8T256GroupM : kW8A8GroupM, false)) return rc;
+    return all_seen("w8a8");
+  }
+  if (op == 2) {  // W4A4 / block-32 int8 (128 x 128 tiles; split-K as grid.y)
+    if (K < 32 || K % 32 != 0 || N <= 0 || splits < 1 || splits > kW4A4MaxSplits)
+      return fail(QL_ERR_SHAPE, "W4A4 needs K %% 32 == 0, N > 0 and splits in [1, %d]", kW4A4MaxSplits);
+    fresh((int)((M + 127) / 128), (int)((N + 127) / 128), 1);
+    if (int rc = launch("w4a4", tiles_m * tiles_n, 0, 1, 1, 128, 128, kW4A4GroupM, false)) return rc;
+    const int k_tiles = (int)((K / 32 + 3) / 4), per = (k_tiles + splits - 1) / splits;
+    if (splits > 1 && (int64_t)per * splits < k_tiles) return fail(QL_ERR_SHAPE, "w4a4 splits miss k-tiles");
+    return all_seen("w4a4");
+  }
+  return fail(QL_ERR_ARG, "op must be 0 (W4A16), 1 (W8A8) or 2 (W4A4), got %d", op);
 }
 
 int qlinear_w4a16_col_scales(const float* w_scale, float* col_scale, int64_t N, int64_t K, void* stream) {

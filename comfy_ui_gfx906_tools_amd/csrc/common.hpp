@@ -209,7 +209,7 @@ __device__ __forceinline__ void barrier_no_fence() {
 // ---- workgroup -> tile order ---------------------------------------------------------------
 // Workgroups are dispatched round-robin over the 8 XCDs (each with its own L2). Renumber them
 // so that consecutive logical ids run on the same XCD and share A/B panels in its L2.
-__device__ __forceinline__ int xcd_remap(int g, int G) {
+__host__ __device__ __forceinline__ int xcd_remap(int g, int G) {
   constexpr int kXcd = 8;
   const int xcd = g % kXcd, local = g / kXcd;
   const int per = G / kXcd, rem = G % kXcd;
@@ -217,12 +217,12 @@ __device__ __forceinline__ int xcd_remap(int g, int G) {
 }
 
 // Grouped ("super-tile") order: kGroupM tile-rows walk the N tiles together.
-__device__ __forceinline__ void tile_coords(int t, int tiles_m, int tiles_n, int group_m, int& tm,
-                                            int& tn) {
+__host__ __device__ __forceinline__ void tile_coords(int t, int tiles_m, int tiles_n, int group_m, int& tm,
+                                                     int& tn) {
   const int per_group = group_m * tiles_n;
   const int grp = t / per_group;
   const int first_m = grp * group_m;
-  const int gsize = min(tiles_m - first_m, group_m);
+  const int gsize = tiles_m - first_m < group_m ? tiles_m - first_m : group_m;
   const int r = t - grp * per_group;
   tm = first_m + r % gsize;
   tn = r / gsize;

@@ -9,6 +9,14 @@ namespace qlinear {
 
 enum Activation { kActNone = 0, kActGeluTanh = 1 };
 
+// Tile rows that walk the tile columns together in each kernel's grouped tile order
+// (tile_coords in common.hpp); the launch-plan check in capi.cpp enumerates with the same values.
+constexpr int kW4A16GroupM = 8;     // w4a16_gemm.hip, configurations 0-3
+constexpr int kTile256GroupM = 4;   // w4a16_tile256.hip
+constexpr int kW4A4GroupM = 8;      // w4a4_gemm.hip
+constexpr int kW8A8GroupM = 8;      // w8a8_gemm.hip
+constexpr int kW8A8T256GroupM = 4;  // w8a8_tile256.hip
+
 struct W4A16Params {
   const void* x;         // [M, K] bf16 / fp16
   const void* wq;        // [N, K/2] packed int4

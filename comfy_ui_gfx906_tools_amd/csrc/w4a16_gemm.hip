@@ -53,7 +53,7 @@ namespace {
 constexpr int kStageK = 128;        // K per pipeline stage (16-bit elements)
 constexpr int kRowBytes = 256;      // one A row of a stage
 constexpr int kGroupsPerStage = 4;  // 128 / 32
-constexpr int kGroupM = 8;
+constexpr int kGroupM = kW4A16GroupM;
 constexpr int kWaves = 4;
 constexpr int kWN = 4;              // 16-column blocks per wave
 

@@ -39,7 +39,7 @@ typedef float f32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kT256StageK = 64;
 constexpr int kT256NBuf = 3;
-constexpr int kT256GroupM = 4;
+constexpr int kT256GroupM = kTile256GroupM;
 
 template <bool kBf16>
 __device__ __forceinline__ f32x16 mfma32(u32x4 a, u32x4 b, f32x16 c) {

@@ -35,7 +35,7 @@ namespace {
 
 constexpr int kW4BM = 128, kW4BN = 128;
 constexpr int kW4RowBytes = 64;  // code bytes per row per stage (4 int4 blocks or 2 int8 blocks)
-constexpr int kW4GroupM = 8;
+constexpr int kW4GroupM = kW4A4GroupM;
 
 // 8 codes of a dword (K = 2t in the low nibble of byte t, 2t + 1 in the high one) as 8 int8 lanes
 // holding code * 16: low dword = even K, high dword = odd K.

@@ -17,7 +17,7 @@ namespace {
 
 constexpr int kStageK8 = 256;  // int8 K per stage = 256 bytes per A row
 constexpr int kRowBytes8 = 256;
-constexpr int kGroupM8 = 8;
+constexpr int kGroupM8 = kW8A8GroupM;
 
 template <int WM, int WN, int NWM, int NWN>
 __global__ __launch_bounds__(64 * NWM * NWN) void w8a8_gemm_kernel(W8A8Params p) {

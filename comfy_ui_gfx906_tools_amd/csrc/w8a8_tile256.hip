@@ -35,7 +35,7 @@ typedef int i32x16 __attribute__((ext_vector_type(16)));
 
 constexpr int kQ8StageK = 64;  // int8 K (= bytes) per stage
 constexpr int kQ8NBuf = 4;
-constexpr int kQ8GroupM = 4;
+constexpr int kQ8GroupM = kW8A8T256GroupM;
 constexpr int kQ8WavesM = 2, kQ8WavesN = 4, kQ8WM = 4, kQ8WN = 2;
 constexpr int kQ8Waves = kQ8WavesM * kQ8WavesN;
 constexpr int kQ8BM = 32 * kQ8WM * kQ8WavesM, kQ8BN = 32 * kQ8WN * kQ8WavesN;  // 256 x 256

@@ -277,6 +277,19 @@ int qlinear_heads_to_f16(int dtype, const void* o, int64_t H, int64_t L_all, int
 int qlinear_gated_residual(int dtype, void* out, const void* x, const void* gate, const void* y,
                            int64_t M, int64_t K, void* stream);
 
+/* ---------------------------------------------------------------------------------------
+ * Host-only self-check of the launch plans (no GPU needed, nothing launched). No counterpart in
+ * the reference. For op 0 (qlinear_w4a16_gemm, any x_dtype / splits / flags), 1
+ * (qlinear_w8a8_gemm) or 2 (qlinear_w4a4_gemm with `splits` >= 1) and a CU count `cus`, walks
+ * every workgroup of every launch the entry point would make through the kernels' own
+ * workgroup -> tile mapping and returns QL_OK if every output tile (and every K piece or 128-row
+ * half of one) is covered exactly once, every workgroup starts inside M x N (or is a 256 x 256
+ * half wholly past M, which the kernel leaves before any memory access), and the workspace holds
+ * every split-K partial; otherwise a status with the first violation in qlinear_last_error().
+ * ------------------------------------------------------------------------------------- */
+int qlinear_check_launch_plan(int op, int x_dtype, int64_t M, int64_t N, int64_t K, int splits,
+                              int flags, int cus);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,67 @@
+"""Launch plans of the tile kernels checked on the CPU (qlinear_check_launch_plan, no GPU): for
+ragged M and N, every kernel configuration, split count and several CU counts, every workgroup of
+every launch maps through the kernels' own xcd_remap / tile_coords to a tile that starts inside
+M x N (or to a 256 x 256 half wholly past M, which the kernel leaves before any memory access),
+every tile part is covered exactly once, and the workspace holds every split-K partial.
+
+Guards the fault class of a workgroup whose tile lies past the edge of its operands (once: a
+128-row half wholly past M built an activation buffer descriptor with a wrapped range).
+"""
+import itertools
+import os
+
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+LIB = os.path.join(ROOT, "comfy_ui_gfx906_tools_amd", "libqlinear.so")
+
+
+@pytest.fixture(scope="module")
+def lib():
+    if not os.path.exists(LIB):
+        pytest.skip("libqlinear.so not built (python -m comfy_ui_gfx906_tools_amd.build)")
+    from comfy_ui_gfx906_tools_amd import _lib
+    return _lib.load_library(LIB)
+
+
+def _check(lib, *args):
+    rc = lib.qlinear_check_launch_plan(*args)
+    assert rc == 0, f"{args}: {lib.qlinear_last_error().decode()}"
+
+
+MS = [1, 2, 5, 16, 17, 63, 64, 65, 127, 128, 129, 200, 255, 256, 257, 383, 384, 385, 512, 513, 640, 1000, 2049, 4608]
+NS = [16, 100, 255, 256, 257, 520, 777, 3072, 12288]
+CUS = [8, 80, 256, 304]
+
+
+@pytest.mark.parametrize("cus", CUS)
+def test_w4a16_plans_every_configuration(lib, cus):
+    flags_cfg = lambda c: (c + 1) << 8  # noqa: E731 - QL_W4A16_CFG(c)
+    for M, N in itertools.product(MS, NS):
+        for K in (64, 640, 3072):
+            for xdt in (1, 2):  # fp16 / bf16 x
+                _check(lib, 0, xdt, M, N, K, 0, 0, cus)              # automatic choice
+                for c in range(7):
+                    for splits in ((0, 1) if c >= 4 else (0, 1, 2, 7)):
+                        _check(lib, 0, xdt, M, N, K, splits, flags_cfg(c), cus)
+
+
+def test_w4a16_plans_k_tails_and_bf16_mode(lib):
+    for M, N, K in itertools.product([3, 130, 300, 513], [200, 777], [32, 96, 160, 4160]):
+        for flags in (0, 1, 1 | (1 + 1) << 8, (0 + 1) << 8):
+            _check(lib, 0, 2, M, N, K, 0, flags, 256)
+
+
+@pytest.mark.parametrize("cus", CUS)
+def test_w8a8_and_w4a4_plans(lib, cus):
+    for M, N in itertools.product(MS, NS):
+        _check(lib, 1, 0, M, N, 3072, 0, 0, cus)
+        for splits in (1, 2, 3, 8):
+            _check(lib, 2, 0, M, N, 1024, splits, 0, cus)
+
+
+def test_plan_check_reports_violations(lib):
+    """The check itself rejects what it must: a bad op or CU count."""
+    assert lib.qlinear_check_launch_plan(3, 0, 64, 64, 64, 0, 0, 256) != 0
+    assert "op must be" in lib.qlinear_last_error().decode()
+    assert lib.qlinear_check_launch_plan(0, 2, 64, 64, 64, 0, 0, 0) != 0
