@@ -64,6 +64,7 @@ SIGNATURES = {
                                    _c_int, _c_vp, _c_size_t, _c_vp]),
     "qlinear_w4a4_auto_splits": (_c_int, [_c_i64, _c_i64, _c_i64, _c_int]),
     "qlinear_check_launch_plan": (_c_int, [_c_int, _c_int, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int]),
+    "qlinear_w4a16_describe_plan": (_c_int, [_c_int, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int, _c_vp]),
     "qlinear_w4a4_workspace_bytes": (_c_size_t, [_c_i64, _c_i64, _c_i64, _c_int, _c_int]),
     "qlinear_rotate_rows_to_f16": (_c_int, [_c_int, _c_vp, _c_vp, _c_int, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
     "qlinear_heads_to_f16": (_c_int, [_c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64, _c_vp,
@@ -271,6 +272,20 @@ def w4a16_gemm(x: torch.Tensor, w_q4: torch.Tensor, w_scale: torch.Tensor, bias:
                                     ws.numel() if ws is not None else 0, stream)
     _check(rc, "w4a16_gemm")
     return y
+
+
+def w4a16_describe_plan(M: int, N: int, K: int, x_dtype: torch.dtype = torch.bfloat16, splits: int = 0,
+                        config: int | None = None, cus: int | None = None) -> dict:
+    """The launch plan qlinear_w4a16_gemm makes (kernel configuration, tile shape, whole tiles, K
+    pieces, staging), for `cus` compute units (default: the current GPU's). Host only."""
+    if cus is None:
+        cus = torch.cuda.get_device_properties(torch.cuda.current_device()).multi_processor_count
+    flags = 0 if config is None else (int(config) + 1) << W4A16_CFG_SHIFT
+    info = (ctypes.c_int * 7)()
+    _check(load_library().qlinear_w4a16_describe_plan(_DTYPE_CODE[x_dtype], M, N, K, splits, flags, int(cus),
+                                                      ctypes.cast(info, ctypes.c_void_p)), "w4a16_describe_plan")
+    return {"config": info[0], "tile_rows": info[1], "tile_cols": info[2], "whole_tiles": info[3],
+            "tiles": info[4], "k_pieces": info[5], "staged": bool(info[6])}
 
 
 def w4a16_auto_splits(M: int, N: int, K: int, device: torch.device | int | None = None) -> int:

@@ -438,6 +438,22 @@ int qlinear_w4a16_gemm_noalloc(int x_dtype, int out_dtype, const void* x, const 
                             flags, ws, need > 0 ? kNoAllocScratchBytes : 0, stream);
 }
 
+int qlinear_w4a16_describe_plan(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, int flags, int cus,
+                                int* info) {
+  if (!info) return fail(QL_ERR_ARG, "null info pointer");
+  if (cus <= 0 || cus > 4096) return fail(QL_ERR_ARG, "cus must be in [1, 4096], got %d", cus);
+  if (int rc = check_w4a16_args(x_dtype, QL_F32, nullptr, M, N, K, splits, flags)) return rc;
+  const W4A16Plan pl = plan_w4a16(x_dtype, M, N, K, splits, flags, cus);
+  info[0] = pl.cfg;
+  info[1] = pl.BM;
+  info[2] = pl.BN;
+  info[3] = pl.dp_tiles;
+  info[4] = pl.tiles_m * pl.tiles_n;
+  info[5] = pl.ksplit;
+  info[6] = pl.prepass ? 1 : 0;
+  return ok();
+}
+
 int qlinear_check_launch_plan(int op, int x_dtype, int64_t M, int64_t N, int64_t K, int splits, int flags, int cus) {
   if (cus <= 0 || cus > 4096) return fail(QL_ERR_ARG, "cus must be in [1, 4096], got %d", cus);
   if (M <= 0) return fail(QL_ERR_ARG, "M must be > 0 for a plan check, got %lld", (long long)M);

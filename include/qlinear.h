@@ -289,6 +289,12 @@ int qlinear_gated_residual(int dtype, void* out, const void* x, const void* gate
  * ------------------------------------------------------------------------------------- */
 int qlinear_check_launch_plan(int op, int x_dtype, int64_t M, int64_t N, int64_t K, int splits,
                               int flags, int cus);
+/* The plan qlinear_w4a16_gemm makes on a device with `cus` compute units, host only: info[0] =
+ * kernel configuration (0-8), [1] / [2] = tile rows / columns, [3] = tiles run whole, [4] = tiles,
+ * [5] = K pieces of each remaining tile, [6] = 1 when x is staged to fp16 first. No counterpart in
+ * the reference (its tile shape is fixed). */
+int qlinear_w4a16_describe_plan(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, int flags,
+                                int cus, int* info);
 
 #ifdef __cplusplus
 }

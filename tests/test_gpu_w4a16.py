@@ -427,3 +427,4 @@ def test_w4a16_skinny_16bit_out_gelu_and_row_scale(out_dtype):
     y = to_np_f32(L.w4a16_gemm(x16, wq.to(DEV), ws.to(DEV), bias.to(DEV), out_dtype=out_dtype, row_scale=rs,
                                config=SKINNY_CFG))
     assert (np.abs(y - ref_r) <= ulp + 2e-4 * np.abs(ref).max()).all()
+

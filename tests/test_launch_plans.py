@@ -65,3 +65,18 @@ def test_plan_check_reports_violations(lib):
     assert lib.qlinear_check_launch_plan(3, 0, 64, 64, 64, 0, 0, 256) != 0
     assert "op must be" in lib.qlinear_last_error().decode()
     assert lib.qlinear_check_launch_plan(0, 2, 64, 64, 64, 0, 0, 0) != 0
+
+
+
+def test_describe_plan():
+    """qlinear_w4a16_describe_plan reports the plan the GEMM makes: the C2 shapes on 256 CUs."""
+    from comfy_ui_gfx906_tools_amd import _lib
+    if not os.path.exists(LIB):
+        pytest.skip("libqlinear.so not built")
+    fc1 = _lib.w4a16_describe_plan(4608, 12288, 3072, cus=256)
+    assert (fc1["config"], fc1["tile_rows"], fc1["tiles"], fc1["whole_tiles"], fc1["staged"]) == (5, 256, 864, 768, True)
+    fc2 = _lib.w4a16_describe_plan(4608, 3072, 12288, cus=256, x_dtype=__import__("torch").float16)
+    assert (fc2["config"], fc2["tiles"], fc2["whole_tiles"], fc2["staged"]) == (5, 216, 216, False)
+    assert _lib.w4a16_describe_plan(1, 10240, 4096, cus=256)["config"] == 7
+    assert _lib.w4a16_describe_plan(16, 10240, 4096, cus=256)["config"] == 8
+    assert _lib.w4a16_describe_plan(64, 10240, 4096, cus=256)["config"] == 2
