@@ -25,6 +25,7 @@ _DTYPE_CODE = {torch.float32: QL_F32, torch.float16: QL_F16, torch.bfloat16: QL_
 
 W4A16_BF16_MFMA = 1  # flags: bf16 activations straight into bf16 MFMA (see include/qlinear.h)
 W4A16_GELU_TANH = 2  # flags: fused GELU-tanh epilogue
+W4A16_F16_ROWSCALED = 4  # flags: output stored as the next GEMM's row-scaled fp16 operand
 W4A16_CFG_SHIFT = 8  # flags bits 8-11: forced kernel configuration + 1 (QL_W4A16_CFG)
 W4A16_TILE256 = 4    # configuration id of the 256 x 256, 8-wave kernel
 W4A16_NOALLOC_SCRATCH_BYTES = 32 << 20  # QL_W4A16_NOALLOC_SCRATCH_BYTES
@@ -45,11 +46,12 @@ SIGNATURES = {
     "qlinear_last_error": (ctypes.c_char_p, []),
     "qlinear_abi_version": (_c_int, []),
     "qlinear_w4a16_workspace_bytes": (_c_size_t, [_c_int, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int]),
-    "qlinear_w4a16_gemm": (_c_int, [_c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64,
-                                    _c_i64, _c_i64, _c_int, _c_int, _c_vp, _c_size_t, _c_vp]),
+    "qlinear_w4a16_gemm": (_c_int, [_c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
+                                    _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_vp, _c_size_t, _c_vp]),
     "qlinear_w4a16_col_scales": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
-    "qlinear_w4a16_gemm_noalloc": (_c_int, [_c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64,
-                                            _c_i64, _c_i64, _c_int, _c_int, _c_vp]),
+    "qlinear_w4a16_out_bound": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_i64, _c_i64, _c_vp, _c_vp]),
+    "qlinear_w4a16_gemm_noalloc": (_c_int, [_c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
+                                            _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_vp]),
     "qlinear_rows_to_f16": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
     "qlinear_w4a16_auto_splits": (_c_int, [_c_i64, _c_i64, _c_i64, _c_int]),
     "qlinear_quantize_int4": (_c_int, [_c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
@@ -173,6 +175,50 @@ def w4a16_col_scales(w_scale: torch.Tensor) -> torch.Tensor:
     return cs
 
 
+def w4a16_out_bound(w_q4: torch.Tensor, w_scale: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
+    """{max_n ||dequant W_n||_1 (1 + 2^-10), max_n |bias_n|} (fp32 [2] on the weight's device): the
+    bound the row-scaled fp16 output (w4a16_gemm(..., f16_rowscaled=True)) derives its row factors
+    from."""
+    lib = load_library()
+    w_q4 = _dev_tensor(w_q4, "w_q4")
+    w_scale = _dev_tensor(w_scale, "w_scale")
+    N = w_q4.shape[0]
+    K = w_q4.shape[1] * 2
+    if w_scale.dtype != torch.float32 or w_scale.numel() != N * (K // 32):
+        raise RuntimeError(f"w_scale must be float32 [{N}, {K // 32}], got {w_scale.dtype} {tuple(w_scale.shape)}")
+    if bias is not None:
+        bias = _dev_tensor(bias, "bias")
+        if bias.numel() != N or bias.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+            raise RuntimeError(f"bias must be a float [{N}] tensor, got {bias.dtype} {tuple(bias.shape)}")
+    buf = torch.empty((2 + (N + 3) // 4,), dtype=torch.float32, device=w_q4.device)
+    with torch.cuda.device(w_q4.device):
+        rc = lib.qlinear_w4a16_out_bound(w_q4.data_ptr(), w_scale.data_ptr(),
+                                         bias.data_ptr() if bias is not None else None,
+                                         _DTYPE_CODE[bias.dtype] if bias is not None else QL_F32, N, K,
+                                         buf.data_ptr(), _stream_ptr(w_q4.device))
+    _check(rc, "w4a16_out_bound")
+    return buf[:2]
+
+
+def cached_out_bound(w_q4: torch.Tensor, w_scale: torch.Tensor, bias: torch.Tensor | None) -> torch.Tensor:
+    """w4a16_out_bound kept on the w_q4 tensor object, recomputed when w_q4, w_scale or bias change
+    (version counters, identity) or the stream differs."""
+    try:
+        key = (w_q4._version, id(w_scale), w_scale._version, id(bias), bias._version if bias is not None else 0,
+               _stream_ptr(w_q4.device))
+    except RuntimeError:  # inference-mode tensors keep no version counter
+        return w4a16_out_bound(w_q4, w_scale, bias)
+    hit = getattr(w_q4, "_qlinear_out_bound", None)
+    if hit is not None and hit[0] == key:
+        return hit[1]
+    b = w4a16_out_bound(w_q4, w_scale, bias)
+    try:
+        w_q4._qlinear_out_bound = (key, b)
+    except (AttributeError, RuntimeError):
+        pass
+    return b
+
+
 def cached_col_scales(w_scale: torch.Tensor) -> torch.Tensor | None:
     """w4a16_col_scales(w_scale), kept on the w_scale tensor object and recomputed when the tensor
     is modified in place (torch's version counter), moved, or used from another stream. None for
@@ -197,7 +243,8 @@ def cached_col_scales(w_scale: torch.Tensor) -> torch.Tensor | None:
 def w4a16_gemm(x: torch.Tensor, w_q4: torch.Tensor, w_scale: torch.Tensor, bias: torch.Tensor | None = None,
                out_dtype: torch.dtype | None = None, splits: int = 0, bf16_mfma: bool = False,
                row_scale: torch.Tensor | None = None, config: int | None = None,
-               gelu: bool = False, col_scale: torch.Tensor | None = None, noalloc: bool = False) -> torch.Tensor:
+               gelu: bool = False, col_scale: torch.Tensor | None = None, noalloc: bool = False,
+               f16_rowscaled: bool = False, out_bound: torch.Tensor | None = None):
     """y[M, N] = x[M, K] @ dequant(w_q4, w_scale)^T (+ bias) on the gfx950 W4A16 kernel.
     x: fp16/bf16/fp32 [M, K]; w_q4: int8 [N, K/2]; w_scale: fp32 [N, K/32]; bias: out_dtype [N].
     bf16 and fp32 activations go through the exact row-scaled fp16 staging unless bf16_mfma is
@@ -208,7 +255,10 @@ def w4a16_gemm(x: torch.Tensor, w_q4: torch.Tensor, w_scale: torch.Tensor, bias:
     col_scale: the fp16 dequant's column factors (w4a16_col_scales of this w_scale); None = the
     GEMM computes them in its workspace.
     noalloc: run qlinear_w4a16_gemm_noalloc (the library's static scratch instead of a workspace
-    from torch's allocator; calls needing more than QL_W4A16_NOALLOC_SCRATCH_BYTES raise)."""
+    from torch's allocator; calls needing more than QL_W4A16_NOALLOC_SCRATCH_BYTES raise).
+    f16_rowscaled: the bf16 result (out_dtype must be bfloat16) stored as the next GEMM's row-scaled
+    fp16 operand (QL_W4A16_F16_ROWSCALED); returns (y16 fp16 [M, N], row_scale fp32 [M]) to pass on
+    as (x, row_scale). out_bound: w4a16_out_bound of this weight and bias (computed when None)."""
     lib = load_library()
     x = _dev_tensor(x, "x")
     w_q4 = _dev_tensor(w_q4, "w_q4")
@@ -233,10 +283,19 @@ def w4a16_gemm(x: torch.Tensor, w_q4: torch.Tensor, w_scale: torch.Tensor, bias:
         bias = _dev_tensor(bias, "bias")
         if bias.dtype != out_dtype or bias.numel() != N:
             raise RuntimeError(f"bias must be {out_dtype} [{N}], got {bias.dtype} {tuple(bias.shape)}")
-    y = torch.empty((M, N), dtype=out_dtype, device=x.device)
+    y = torch.empty((M, N), dtype=torch.float16 if f16_rowscaled else out_dtype, device=x.device)
+    out_rs = None
+    if f16_rowscaled:
+        if out_dtype != torch.bfloat16:
+            raise RuntimeError(f"f16_rowscaled rounds to bfloat16; out_dtype {out_dtype} given")
+        out_rs = torch.empty((M,), dtype=torch.float32, device=x.device)
+        if out_bound is None:
+            out_bound = w4a16_out_bound(w_q4, w_scale, bias)
+        out_bound = _dev_tensor(out_bound, "out_bound")
     if M == 0:
-        return y
-    flags = (W4A16_BF16_MFMA if bf16_mfma else 0) | (W4A16_GELU_TANH if gelu else 0)
+        return (y, out_rs) if f16_rowscaled else y
+    flags = (W4A16_BF16_MFMA if bf16_mfma else 0) | (W4A16_GELU_TANH if gelu else 0) | \
+        (W4A16_F16_ROWSCALED if f16_rowscaled else 0)
     if config is not None:
         flags |= (int(config) + 1) << W4A16_CFG_SHIFT
     xdt = _DTYPE_CODE[x.dtype]
@@ -257,21 +316,25 @@ def w4a16_gemm(x: torch.Tensor, w_q4: torch.Tensor, w_scale: torch.Tensor, bias:
                                                 row_scale.data_ptr() if row_scale is not None else None,
                                                 w_q4.data_ptr(), w_scale.data_ptr(),
                                                 col_scale.data_ptr() if col_scale is not None else None,
-                                                bias.data_ptr() if bias is not None else None, y.data_ptr(), M, N, K,
+                                                bias.data_ptr() if bias is not None else None, y.data_ptr(),
+                                                out_bound.data_ptr() if out_bound is not None else None,
+                                                out_rs.data_ptr() if out_rs is not None else None, M, N, K,
                                                 splits, flags, stream)
             _check(rc, "w4a16_gemm_noalloc")
-            return y
+            return (y, out_rs) if f16_rowscaled else y
         nbytes = lib.qlinear_w4a16_workspace_bytes(xdt, M, N, K, splits, flags, x.device.index)
         ws = _workspaces.get(x.device, stream, nbytes) if nbytes else None
         rc = lib.qlinear_w4a16_gemm(xdt, _DTYPE_CODE[out_dtype], x.data_ptr(),
                                     row_scale.data_ptr() if row_scale is not None else None,
                                     w_q4.data_ptr(), w_scale.data_ptr(),
                                     col_scale.data_ptr() if col_scale is not None else None,
-                                    bias.data_ptr() if bias is not None else None, y.data_ptr(), M, N, K, splits,
+                                    bias.data_ptr() if bias is not None else None, y.data_ptr(),
+                                    out_bound.data_ptr() if out_bound is not None else None,
+                                    out_rs.data_ptr() if out_rs is not None else None, M, N, K, splits,
                                     flags, ws.data_ptr() if ws is not None else None,
                                     ws.numel() if ws is not None else 0, stream)
     _check(rc, "w4a16_gemm")
-    return y
+    return (y, out_rs) if f16_rowscaled else y
 
 
 def w4a16_describe_plan(M: int, N: int, K: int, x_dtype: torch.dtype = torch.bfloat16, splits: int = 0,

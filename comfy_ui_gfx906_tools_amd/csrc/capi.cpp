@@ -152,7 +152,8 @@ int skinny_blocks(int64_t M, int64_t N, int cus) {
 // QL_W4A16_BF16_MFMA asks for the reference's bf16-rounded weights, which only the tile kernels
 // compute; 7 and 8 use the exact codes and are skipped then.
 int w4a16_cfg_for(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, int flags, int cus) {
-  const bool exact_ok = splits < 2 && !(flags & QL_W4A16_BF16_MFMA);
+  // the direct kernels (7, 8) neither compute the bf16-rounded weights nor store row-scaled fp16
+  const bool exact_ok = splits < 2 && !(flags & (QL_W4A16_BF16_MFMA | QL_W4A16_F16_ROWSCALED));
   if (exact_ok && M <= 1 && gemv_fits(x_dtype, M, K)) return kCfgGemv;
   if (exact_ok && skinny_fits(x_dtype, M, N, K)) return kCfgSkinny;
   if (exact_ok && gemv_fits(x_dtype, M, K)) return kCfgGemv;
@@ -255,8 +256,20 @@ int check_w4a16_args(int x_dtype, int out_dtype, const float* row_scale, int64_t
                 out_dtype);
   if (int rc = check_w4a16_shape(M, N, K)) return rc;
   if (splits < 0 || splits > 64) return fail(QL_ERR_ARG, "splits must be in [0, 64], got %d", splits);
-  if (flags & ~(QL_W4A16_BF16_MFMA | QL_W4A16_GELU_TANH | QL_W4A16_CFG_MASK))
+  if (flags & ~(QL_W4A16_BF16_MFMA | QL_W4A16_GELU_TANH | QL_W4A16_F16_ROWSCALED | QL_W4A16_CFG_MASK))
     return fail(QL_ERR_ARG, "unknown flags 0x%x", flags);
+  if (flags & QL_W4A16_F16_ROWSCALED) {
+    const int forced = (flags & QL_W4A16_CFG_MASK) >> QL_W4A16_CFG_SHIFT;
+    if (out_dtype != QL_BF16)
+      return fail(QL_ERR_ARG, "QL_W4A16_F16_ROWSCALED rounds to the logical output dtype bfloat16 (out dtype %s given)",
+                  dtype_name(out_dtype));
+    if ((flags & QL_W4A16_BF16_MFMA) || (x_dtype == QL_F16 && !row_scale))
+      return fail(QL_ERR_ARG, "QL_W4A16_F16_ROWSCALED bounds each output row by its input row factor: it needs "
+                  "float16 x with row_scale, or bfloat16 / float32 x on the fp16 staging route");
+    if (forced && forced - 1 > 3 && forced - 1 != kCfgTile256Auto)
+      return fail(QL_ERR_ARG, "QL_W4A16_F16_ROWSCALED runs on kernel configurations 0-3 and %d, not %d",
+                  kCfgTile256Auto, forced - 1);
+  }
   {
     const int forced = (flags & QL_W4A16_CFG_MASK) >> QL_W4A16_CFG_SHIFT;
     if (forced > kCfgLast + 1) return fail(QL_ERR_ARG, "flags: kernel configuration %d does not exist (0-%d)",
@@ -298,6 +311,16 @@ int w4a4_reference_splits(int64_t M, int64_t N, int64_t K, int cus) {
   return (int)std::min(wanted, max_splits);
 }
 
+// The argument checks that do not depend on the call's pointers, for the host-only queries
+// (workspace size, plan description, plan check): the row-scaled fp16 output is taken with its
+// required bfloat16 logical dtype and, for fp16 x, a row_scale.
+int check_w4a16_plan_args(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, int flags) {
+  static const float kSomeRowScale = 1.0f;
+  const bool rowscaled = (flags & QL_W4A16_F16_ROWSCALED) != 0;
+  return check_w4a16_args(x_dtype, rowscaled ? QL_BF16 : QL_F32, (rowscaled && x_dtype == QL_F16) ? &kSomeRowScale : nullptr,
+                          M, N, K, splits, flags);
+}
+
 // ---- static scratch of the allocation-free W4A16 entry point ---------------------------------
 // qlinear_w4a16_gemm_noalloc runs the same plan as qlinear_w4a16_gemm with this array as its
 // workspace. Every GPU the library runs on holds its own copy (its code object's, loaded with the
@@ -336,7 +359,7 @@ int qlinear_abi_version(void) { return (2 << 16) | 0; }
 size_t qlinear_w4a16_workspace_bytes(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, int flags,
                                      int device) {
   // invalid arguments (a forced configuration that does not exist among them) plan nothing
-  if (check_w4a16_args(x_dtype, QL_F32, nullptr, M, N, K, splits, flags) != QL_OK || M == 0) return 0;
+  if (check_w4a16_plan_args(x_dtype, M, N, K, splits, flags) != QL_OK || M == 0) return 0;
   int cus = 0;
   if (device_cus(device, &cus) != QL_OK) return 0;
   return plan_w4a16(x_dtype, M, N, K, splits, flags, cus).total;
@@ -352,9 +375,12 @@ int qlinear_w4a16_auto_splits(int64_t M, int64_t N, int64_t K, int device) {
 }
 
 int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const float* row_scale, const void* w_q4,
-                       const float* w_scale, const float* col_scale, const void* bias, void* y, int64_t M, int64_t N,
-                       int64_t K, int splits, int flags, void* workspace, size_t workspace_bytes, void* stream) {
+                       const float* w_scale, const float* col_scale, const void* bias, void* y, const float* out_bound,
+                       float* out_row_scale, int64_t M, int64_t N, int64_t K, int splits, int flags, void* workspace,
+                       size_t workspace_bytes, void* stream) {
   if (int rc = check_w4a16_args(x_dtype, out_dtype, row_scale, M, N, K, splits, flags)) return rc;
+  if ((flags & QL_W4A16_F16_ROWSCALED) && M > 0 && (!out_bound || !out_row_scale))
+    return fail(QL_ERR_ARG, "QL_W4A16_F16_ROWSCALED needs out_bound (qlinear_w4a16_out_bound) and out_row_scale [M]");
   if (M == 0) return ok();
   if (!x || !w_q4 || !w_scale || !y) return fail(QL_ERR_ARG, "null x / w_q4 / w_scale / y pointer");
   if (!aligned16(x) || !aligned16(w_q4))
@@ -398,7 +424,9 @@ int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const float* r
   p.M = (int)M;
   p.N = (int)N;
   p.K = (int)K;
-  p.out_dtype = out_dtype;
+  p.out_dtype = (flags & QL_W4A16_F16_ROWSCALED) ? kBF16AsF16 : out_dtype;
+  p.out_bound = out_bound;
+  p.out_row_scale = out_row_scale;
   p.act = (flags & QL_W4A16_GELU_TANH) ? kActGeluTanh : kActNone;
   p.cus = cus;
   p.tiles_m = pl.tiles_m;
@@ -417,8 +445,9 @@ int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const float* r
 }
 
 int qlinear_w4a16_gemm_noalloc(int x_dtype, int out_dtype, const void* x, const float* row_scale, const void* w_q4,
-                               const float* w_scale, const float* col_scale, const void* bias, void* y, int64_t M,
-                               int64_t N, int64_t K, int splits, int flags, void* stream) {
+                               const float* w_scale, const float* col_scale, const void* bias, void* y,
+                               const float* out_bound, float* out_row_scale, int64_t M, int64_t N, int64_t K,
+                               int splits, int flags, void* stream) {
   // the checks qlinear_w4a16_gemm makes before planning, so the size check below sees a valid plan
   if (int rc = check_w4a16_args(x_dtype, out_dtype, row_scale, M, N, K, splits, flags)) return rc;
   if (M == 0) return ok();
@@ -434,15 +463,15 @@ int qlinear_w4a16_gemm_noalloc(int x_dtype, int out_dtype, const void* x, const 
   if (need > 0) {
     if (int rc = scratch_address(&ws)) return rc;
   }
-  return qlinear_w4a16_gemm(x_dtype, out_dtype, x, row_scale, w_q4, w_scale, col_scale, bias, y, M, N, K, splits,
-                            flags, ws, need > 0 ? kNoAllocScratchBytes : 0, stream);
+  return qlinear_w4a16_gemm(x_dtype, out_dtype, x, row_scale, w_q4, w_scale, col_scale, bias, y, out_bound,
+                            out_row_scale, M, N, K, splits, flags, ws, need > 0 ? kNoAllocScratchBytes : 0, stream);
 }
 
 int qlinear_w4a16_describe_plan(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, int flags, int cus,
                                 int* info) {
   if (!info) return fail(QL_ERR_ARG, "null info pointer");
   if (cus <= 0 || cus > 4096) return fail(QL_ERR_ARG, "cus must be in [1, 4096], got %d", cus);
-  if (int rc = check_w4a16_args(x_dtype, QL_F32, nullptr, M, N, K, splits, flags)) return rc;
+  if (int rc = check_w4a16_plan_args(x_dtype, M, N, K, splits, flags)) return rc;
   const W4A16Plan pl = plan_w4a16(x_dtype, M, N, K, splits, flags, cus);
   info[0] = pl.cfg;
   info[1] = pl.BM;
@@ -501,7 +530,7 @@ int qlinear_check_launch_plan(int op, int x_dtype, int64_t M, int64_t N, int64_t
     return QL_OK;
   };
   if (op == 0) {  // W4A16 (qlinear_w4a16_gemm's plan)
-    if (int rc = check_w4a16_args(x_dtype, QL_F32, nullptr, M, N, K, splits, flags)) return rc;
+    if (int rc = check_w4a16_plan_args(x_dtype, M, N, K, splits, flags)) return rc;
     const W4A16Plan pl = plan_w4a16(x_dtype, M, N, K, splits, flags, cus);
     const int tiles = pl.tiles_m * pl.tiles_n;
     if (pl.cfg == kCfgGemv || pl.cfg == kCfgSkinny) {
@@ -576,6 +605,20 @@ int qlinear_check_launch_plan(int op, int x_dtype, int64_t M, int64_t N, int64_t
     return all_seen("w4a4");
   }
   return fail(QL_ERR_ARG, "op must be 0 (W4A16), 1 (W8A8) or 2 (W4A4), got %d", op);
+}
+
+int qlinear_w4a16_out_bound(const void* w_q4, const float* w_scale, const void* bias, int bias_dtype, int64_t N,
+                            int64_t K, float* bound, void* stream) {
+  if (N <= 0 || K < 32 || K % 32 != 0 || N > INT32_MAX / 2 || K > (1 << 22))
+    return fail(QL_ERR_SHAPE, "expected w_q4 [N, K/2], w_scale [N, K/32] with K %% 32 == 0, N > 0; got N=%lld K=%lld",
+                (long long)N, (long long)K);
+  if (bias && bias_dtype != QL_F32 && bias_dtype != QL_F16 && bias_dtype != QL_BF16)
+    return fail(QL_ERR_DTYPE, "bias dtype %s (%d) unsupported", dtype_name(bias_dtype), bias_dtype);
+  if (!w_q4 || !w_scale || !bound) return fail(QL_ERR_ARG, "null w_q4 / w_scale / bound pointer");
+  if (!aligned16(w_q4)) return fail(QL_ERR_ALIGN, "w_q4 must be 16-byte aligned");
+  const hipError_t e = w4a16_out_bound_launch(w_q4, w_scale, bias, bias_dtype, N, K, bound, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(QL_ERR_LAUNCH, "w4a16_out_bound launch failed: %s", hipGetErrorString(e));
+  return ok();
 }
 
 int qlinear_w4a16_col_scales(const float* w_scale, float* col_scale, int64_t N, int64_t K, void* stream) {

@@ -16,6 +16,32 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 enum DType { kF32 = 0, kF16 = 1, kBF16 = 2, kI32 = 3 };
+// Epilogue-internal output mode of the W4A16 kernels: each value is rounded to bf16 (the logical
+// output dtype) and stored as the exact fp16 number value * 2^-e_m of its row m (see
+// f16_row_factor), so the next GEMM takes it as its row-scaled fp16 operand without a staging pass.
+constexpr int kBF16AsF16 = 5;
+
+// The fp16 storage factor of an output row whose values are bounded in magnitude by b: down = 2^-e
+// and up = 2^e with b * 2^-e in [2^14, 2^15) (e clamped to [-126, 126]; 1 for b = 0 or not finite).
+// A bf16 value v with |v| <= b then maps to v * 2^-e <= 2^15 (1 + 2^-8) < 65504 exactly whenever
+// |v| >= 2^(e - 17): the rows' values within 2^-31 of the bound keep all their bits.
+__device__ __forceinline__ void f16_row_factor(float b, float& down, float& up) {
+  int e = 0;
+  if (b > 0.0f && b <= 3.4028235e38f) {
+    int E;
+    frexpf(b, &E);  // b = f 2^E, f in [0.5, 1)
+    e = min(max(E - 15, -126), 126);
+  }
+  down = ldexpf(1.0f, -e);
+  up = ldexpf(1.0f, e);
+}
+// The bound of an output row of x @ W^T + bias (optionally through GELU) from the row's input
+// factor rs (max |x[m, :]| < 2^15 rs, as every row-scaled fp16 operand here guarantees) and the
+// weight's bound {max_n sum_k |W_nk|, max_n |bias_n|}: |y| <= 2^15 rs max_n ||W_n||_1 + max|bias|,
+// and |gelu(v)| <= max(|v|, 0.17). Rounding of this fp32 evaluation is covered by the 1e-4 factor.
+__device__ __forceinline__ float w4a16_row_bound(float rs, float wl1, float bmax) {
+  return (32768.0f * rs * wl1) * 1.0001f + bmax + 0.17f;
+}
 
 constexpr int kWave = 64;
 constexpr int kGroup = 32;  // int4 quant group along K (ops.py BLOCK = 32)

@@ -28,6 +28,10 @@ struct W4A16Params {
   // group scales of column n are multiplied by 2^-e_n before the fp16 rounding of q * s and the
   // epilogue multiplies by 2^e_n, so every column's dequantized weights sit in fp16's normal range
   const float* col_scale;
+  // out_dtype kBF16AsF16: {max_n ||W_n||_1, max_n |bias_n|} (w4a16_out_bound_launch) and the
+  // output's fp16 row factors 2^e_m [M], written by the kernels
+  const float* out_bound;
+  float* out_row_scale;
   float* partial;        // partial tiles of the cut tiles: (tiles - dp_tiles) * ksplit slots of BM * BN fp32
   int M, N, K;
   int out_dtype;
@@ -70,6 +74,10 @@ hipError_t rows_to_scaled_f16_launch(int dtype, const void* x, void* x16, float*
 // col_scale[n] = 2^e_n with 8 max_g |w_scale[n, g]| * 2^-e_n in [2^14, 2^15), e_n clamped to
 // [-126, 126]; 1 for a column whose scales are all zero or not finite (w4a16_gemm.hip).
 hipError_t col_scales_launch(const float* w_scale, float* col_scale, int64_t N, int64_t groups, hipStream_t stream);
+// bound[0] = max_n sum_k |q_nk s_n,k/32| (1 + 2^-10), bound[1] = max_n |bias_n| (0 without bias);
+// bound[2 ..] holds per-workgroup partial maxima, (N + 3) / 4 floats (w4a16_gemm.hip).
+hipError_t w4a16_out_bound_launch(const void* w_q4, const float* w_scale, const void* bias, int bias_dtype, int64_t N,
+                                  int64_t K, float* bound, hipStream_t stream);
 
 struct W8A8Params {
   const int8_t* xq;      // [M, K]

@@ -345,7 +345,9 @@ __global__ __launch_bounds__(64 * kWaves) void w4a16_gemm_kernel(W4A16Params p) 
   for (int fn = 0; fn < WN; ++fn) {
     const int n = dst_n0 + (wn * WN + fn) * 16 + 4 * j4;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) bv[fn][e] = (bias && n + e < dst_N) ? read_elem(bias, p.out_dtype, n + e) : 0.0f;
+    for (int e = 0; e < 4; ++e)
+      bv[fn][e] = (bias && n + e < dst_N) ? read_elem(bias, p.out_dtype == kBF16AsF16 ? kBF16 : p.out_dtype, n + e)
+                                          : 0.0f;
   }
   // The wave's output columns are the columns of its K loop (csd). When every one has factor 1
   // (ordinary checkpoints) the plain epilogue runs; the choice is uniform over the wave.
@@ -367,6 +369,15 @@ __global__ __launch_bounds__(64 * kWaves) void w4a16_gemm_kernel(W4A16Params p) 
       const int m = dst_m0 + fm * 16 + r16;
       if (m < dst_M) {
         const float rs = row_scale ? row_scale[m] : 1.0f;
+        // kBF16AsF16: the row's fp16 storage factor from its bound (see f16_row_factor); the
+        // tile column 0 workgroup's wave 0 publishes 2^e_m
+        const int rnd = dst_dtype == kBF16AsF16 ? (int)kBF16 : dst_dtype;
+        float rdown = 1.0f;
+        if (dst_dtype == kBF16AsF16) {
+          float up;
+          f16_row_factor(w4a16_row_bound(rs, p.out_bound[0], p.out_bound[1]), rdown, up);
+          if (tn == 0 && wn == 0 && j4 == 0) p.out_row_scale[m] = up;
+        }
 #pragma unroll
         for (int fn = 0; fn < WN; ++fn) {
           const int n = dst_n0 + (wn * WN + fn) * 16 + 4 * j4;
@@ -374,15 +385,17 @@ __global__ __launch_bounds__(64 * kWaves) void w4a16_gemm_kernel(W4A16Params p) 
 #pragma unroll
           for (int e = 0; e < 4; ++e) {
             v[e] = kColScaled ? acc[fm][fn][e] * rs * cu[fn][e] + bv[fn][e] : acc[fm][fn][e] * rs + bv[fn][e];
-            if (dst_act == kActGeluTanh) v[e] = gelu_tanh(round_to(dst_dtype, v[e]));
+            if (dst_act == kActGeluTanh) v[e] = gelu_tanh(round_to(rnd, v[e]));
+            if (dst_dtype == kBF16AsF16) v[e] = round_to(kBF16, v[e]) * rdown;  // exact in fp16
           }
           const size_t off = (size_t)m * dst_N + n;
+          const int st = dst_dtype == kBF16AsF16 ? (int)kF16 : dst_dtype;  // storage dtype
           if (vec && n + 3 < dst_N) {
-            if (dst_dtype == kF32) {
+            if (st == kF32) {
               *(f32x4*)((float*)dst + off) = f32x4{v[0], v[1], v[2], v[3]};
             } else {
               typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
-              const bool bf = dst_dtype == kBF16;
+              const bool bf = st == kBF16;
               const u32x2 w = {bf ? pack2_bf16(v[0], v[1]) : pack2_f16(v[0], v[1]),
                                bf ? pack2_bf16(v[2], v[3]) : pack2_f16(v[2], v[3])};
               *(u32x2*)((uint16_t*)dst + off) = w;
@@ -390,7 +403,7 @@ __global__ __launch_bounds__(64 * kWaves) void w4a16_gemm_kernel(W4A16Params p) 
           } else {
 #pragma unroll
             for (int e = 0; e < 4; ++e)
-              if (n + e < dst_N) write_elem(dst, dst_dtype, off + e, v[e]);
+              if (n + e < dst_N) write_elem(dst, st, off + e, v[e]);
           }
         }
       }
@@ -425,6 +438,14 @@ __global__ __launch_bounds__(256) void w4a16_reduce_kernel(W4A16Params p, int BM
   const int m = tm * BM + idx / BN;
   if (m >= p.M) return;
   const float rs = p.row_scale ? p.row_scale[m] : 1.0f;
+  const bool as_f16 = p.out_dtype == kBF16AsF16;
+  const int rnd = as_f16 ? (int)kBF16 : p.out_dtype;  // the logical output dtype
+  float rdown = 1.0f;
+  if (as_f16) {  // the row's fp16 storage factor; the thread holding the tile's column 0 publishes it
+    float up;
+    f16_row_factor(w4a16_row_bound(rs, p.out_bound[0], p.out_bound[1]), rdown, up);
+    if (tn == 0 && idx % BN == 0) p.out_row_scale[m] = up;
+  }
   const int n0 = tn * BN + idx % BN;  // a multiple of 4
   f32x4 cu = {1.0f, 1.0f, 1.0f, 1.0f};
   if (p.col_scale) {
@@ -439,10 +460,11 @@ __global__ __launch_bounds__(256) void w4a16_reduce_kernel(W4A16Params p, int BM
   for (int e = 0; e < 4; ++e) {
     const int n = n0 + e;
     if (n >= p.N) continue;
-    const float bv = p.bias ? read_elem(p.bias, p.out_dtype, n) : 0.0f;
+    const float bv = p.bias ? read_elem(p.bias, rnd, n) : 0.0f;
     float out = v[e] * rs * cu[e] + bv;
-    if (p.act == kActGeluTanh) out = gelu_tanh(round_to(p.out_dtype, out));
-    write_elem(p.y, p.out_dtype, (size_t)m * p.N + n, out);
+    if (p.act == kActGeluTanh) out = gelu_tanh(round_to(rnd, out));
+    if (as_f16) out = round_to(kBF16, out) * rdown;  // exact in fp16
+    write_elem(p.y, as_f16 ? (int)kF16 : p.out_dtype, (size_t)m * p.N + n, out);
   }
 }
 
@@ -577,6 +599,64 @@ __global__ __launch_bounds__(256) void col_scales_kernel(const float* __restrict
   }
 }
 
+// Per-column L1 norms of the dequantized weight, one wave per column (4 per workgroup), and the
+// workgroup's maximum into partial[blockIdx.x]: sum over groups of |s_g| * sum of |codes| (the
+// integer sums are exact; the fp32 products and sum round, which the 2^-10 margin of the final
+// bound covers for K up to 2^22).
+__global__ __launch_bounds__(256) void w4a16_col_l1_kernel(const uint8_t* __restrict__ wq, const float* __restrict__ ws,
+                                                           int N, int K, float* __restrict__ partial) {
+  __shared__ float red[4];
+  const int n = blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  float sum = 0.0f;
+  if (n < N) {
+    const int groups = K / kGroup;
+    const uint8_t* row = wq + (size_t)n * (K / 2);
+    for (int g = lane; g < groups; g += kWave) {
+      const u32x4 w = *(const u32x4*)(row + (size_t)g * 16);
+      int a = 0;
+#pragma unroll
+      for (int d = 0; d < 4; ++d)
+#pragma unroll
+        for (int t = 0; t < 8; ++t) {
+          const int c = (int)((w[d] >> (4 * t)) & 0xFu);
+          a += c >= 8 ? 16 - c : c;
+        }
+      sum += fabsf(ws[(size_t)n * groups + g]) * (float)a;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) sum += __shfl_xor(sum, off, kWave);
+  }
+  if (lane == 0) red[threadIdx.x >> 6] = sum;
+  __syncthreads();
+  if (threadIdx.x == 0) partial[blockIdx.x] = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+}
+
+// bound[0] = max over the partial maxima * (1 + 2^-10), bound[1] = max |bias|: one workgroup.
+__global__ __launch_bounds__(256) void w4a16_bound_reduce_kernel(const float* __restrict__ partial, int np,
+                                                                 const void* __restrict__ bias, int bias_dtype, int N,
+                                                                 float* __restrict__ bound) {
+  __shared__ float red[2][4];
+  float a = 0.0f, b = 0.0f;
+  for (int i = threadIdx.x; i < np; i += 256) a = fmaxf(a, partial[i]);
+  if (bias)
+    for (int i = threadIdx.x; i < N; i += 256) b = fmaxf(b, fabsf(read_elem(bias, bias_dtype, (size_t)i)));
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) {
+    a = fmaxf(a, __shfl_xor(a, off, kWave));
+    b = fmaxf(b, __shfl_xor(b, off, kWave));
+  }
+  if ((threadIdx.x & 63) == 0) {
+    red[0][threadIdx.x >> 6] = a;
+    red[1][threadIdx.x >> 6] = b;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    bound[0] = fmaxf(fmaxf(red[0][0], red[0][1]), fmaxf(red[0][2], red[0][3])) * (1.0f + 0x1p-10f);
+    bound[1] = fmaxf(fmaxf(red[1][0], red[1][1]), fmaxf(red[1][2], red[1][3]));
+  }
+}
+
 template <int DT>
 hipError_t rows_launch_r(const void* x, void* x16, float* row_scale, int64_t M, int64_t K, hipStream_t stream) {
   const dim3 grid((unsigned)M), block(256);
@@ -662,6 +742,16 @@ hipError_t rows_to_scaled_f16_launch(int dtype, const void* x, void* x16, float*
     case kF16: return rows_launch_r<kF16>(x, x16, row_scale, M, K, stream);
     default: return rows_launch_r<kBF16>(x, x16, row_scale, M, K, stream);
   }
+}
+
+hipError_t w4a16_out_bound_launch(const void* w_q4, const float* w_scale, const void* bias, int bias_dtype, int64_t N,
+                                  int64_t K, float* bound, hipStream_t stream) {
+  const int np = (int)((N + 3) / 4);
+  hipLaunchKernelGGL(w4a16_col_l1_kernel, dim3((unsigned)np), dim3(256), 0, stream, (const uint8_t*)w_q4, w_scale,
+                     (int)N, (int)K, bound + 2);
+  hipLaunchKernelGGL(w4a16_bound_reduce_kernel, dim3(1), dim3(256), 0, stream, (const float*)(bound + 2), np, bias,
+                     bias_dtype, (int)N, bound);
+  return hipGetLastError();
 }
 
 hipError_t col_scales_launch(const float* w_scale, float* col_scale, int64_t N, int64_t groups, hipStream_t stream) {

@@ -334,7 +334,8 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int n = n0 + wn * 32 * WN + 32 * i + 8 * bq + 4 * h + e;
-        bv[i][bq][e] = (bias_p && n < N) ? read_elem(bias_p, p.out_dtype, n) : 0.0f;
+        bv[i][bq][e] = (bias_p && n < N) ? read_elem(bias_p, p.out_dtype == kBF16AsF16 ? kBF16 : p.out_dtype, n)
+                                         : 0.0f;
       }
   // When every column of the tile has factor 1 (ordinary checkpoints) the plain epilogue runs.
   // Each wave checks all BN columns (BN / 64 per lane), so the choice is uniform over the
@@ -353,11 +354,27 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W
     const int m = m0 + wm * 32 * WM + 32 * j + c32;
     rsj[j] = (rs_p && m < M) ? rs_p[m] : 1.0f;
   }
+  // kBF16AsF16 output: row m is stored as fp16 times 2^-e_m, 2^e_m from the row's bound (its input
+  // row factor and the weight's bound); the tile column 0 workgroups publish 2^e_m, one lane a row.
+  float rdown[WM];
+#pragma unroll
+  for (int j = 0; j < WM; ++j) rdown[j] = 1.0f;
+  if (p.out_dtype == kBF16AsF16) {
+    const float wl1 = p.out_bound[0], bmax = p.out_bound[1];
+#pragma unroll
+    for (int j = 0; j < WM; ++j) {
+      float up;
+      f16_row_factor(w4a16_row_bound(rsj[j], wl1, bmax), rdown[j], up);
+      const int m = m0 + wm * 32 * WM + 32 * j + c32;
+      if (tn == 0 && wn == 0 && h == 0 && m < M) p.out_row_scale[m] = up;
+    }
+  }
   // The epilogue is instantiated per (activation, output dtype), so that its per-value code has no
   // branches; one uniform dispatch selects the instance.
   auto epilogue = [&](auto actc, auto odtc, auto colc) {
     constexpr int kAct = decltype(actc)::value, kOdt = decltype(odtc)::value;
     constexpr bool kColScaled = decltype(colc)::value;
+    constexpr int kRnd = kOdt == kBF16AsF16 ? (int)kBF16 : kOdt;  // the logical output dtype
     float cu[WN][4][4];
 #pragma unroll
     for (int i = 0; i < WN; ++i)
@@ -371,7 +388,8 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W
     auto value = [&](int i, int j, int bq, int e) {
       float v = kColScaled ? acc[i][j][4 * bq + e] * rsj[j] * cu[i][bq][e] + bv[i][bq][e]
                            : acc[i][j][4 * bq + e] * rsj[j] + bv[i][bq][e];
-      if constexpr (kAct == kActGeluTanh) v = gelu_tanh(round_to(kOdt, v));
+      if constexpr (kAct == kActGeluTanh) v = gelu_tanh(round_to(kRnd, v));
+      if constexpr (kOdt == kBF16AsF16) v = round_to(kBF16, v) * rdown[j];  // exact in fp16
       return v;
     };
     if constexpr (kOdt == kF32) {
@@ -428,7 +446,7 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W
               if constexpr (kOdt == kBF16) {
                 lo = pack2_bf16(value(i, j, bq, 0), value(i, j, bq, 1));
                 hi = pack2_bf16(value(i, j, bq, 2), value(i, j, bq, 3));
-              } else {
+              } else {  // fp16, and kBF16AsF16 (values already exact fp16 numbers)
                 lo = pack2_f16(value(i, j, bq, 0), value(i, j, bq, 1));
                 hi = pack2_f16(value(i, j, bq, 2), value(i, j, bq, 3));
               }
@@ -464,6 +482,10 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W
         break;
       case kF16:
         gelu ? epilogue(ic<kActGeluTanh>{}, ic<kF16>{}, colc) : epilogue(ic<kActNone>{}, ic<kF16>{}, colc);
+        break;
+      case kBF16AsF16:  // variant 1 and its halves only (the C ABI rejects it for the others)
+        if constexpr (kWavesM == 1 && kWavesN == 8)
+          gelu ? epilogue(ic<kActGeluTanh>{}, ic<kBF16AsF16>{}, colc) : epilogue(ic<kActNone>{}, ic<kBF16AsF16>{}, colc);
         break;
       default:
         gelu ? epilogue(ic<kActGeluTanh>{}, ic<kBF16>{}, colc) : epilogue(ic<kActNone>{}, ic<kBF16>{}, colc);

@@ -93,11 +93,13 @@ class Staged(NamedTuple):
     dtype: torch.dtype
 
 
-def _linear(layer, x, gelu: bool = False, rows: slice | None = None) -> torch.Tensor:
+def _linear(layer, x, gelu: bool = False, rows: slice | None = None, staged_out: bool = False):
     """layer(x), optionally followed by GELU-tanh, optionally restricted to output rows `rows`
     of the weight. Engine layers fuse the GELU into the GEMM epilogue, take row slices of
     weight_q4 / weight_scale / bias as views (rows of the packed layout are contiguous) and
-    accept a Staged operand."""
+    accept a Staged operand. staged_out: return the bf16 result as the next GEMM's Staged operand
+    (row-scaled fp16 written by this GEMM's epilogue, no staging pass) where the engine can: an
+    engine layer without rotation or row slice, a Staged bf16 input; otherwise a plain tensor."""
     if _is_engine_linear(layer):
         wq, ws, b = layer.weight_q4, layer.weight_scale, layer.bias
         # the fp16 dequant's per-column factors, kept with the whole weight (rows slice them)
@@ -109,8 +111,14 @@ def _linear(layer, x, gelu: bool = False, rows: slice | None = None) -> torch.Te
         if isinstance(x, Staged):
             if layer.rotation_group:
                 raise RuntimeError("a layer with activation rotation takes a plain activation tensor")
-            y = _lib.w4a16_gemm(x.x16, wq, ws, b.to(x.dtype) if b is not None else None, out_dtype=x.dtype,
-                                row_scale=x.row_scale, gelu=gelu, col_scale=cs)
+            bias = b.to(x.dtype) if b is not None else None
+            if staged_out and rows is None and x.dtype == torch.bfloat16:
+                y16, rs = _lib.w4a16_gemm(x.x16, wq, ws, bias, out_dtype=x.dtype, row_scale=x.row_scale, gelu=gelu,
+                                          col_scale=cs, f16_rowscaled=True,
+                                          out_bound=_lib.cached_out_bound(wq, ws, bias))
+                return Staged(y16, rs, x.lead, x.dtype)
+            y = _lib.w4a16_gemm(x.x16, wq, ws, bias, out_dtype=x.dtype, row_scale=x.row_scale, gelu=gelu,
+                                col_scale=cs)
             return y.reshape(*x.lead, wq.shape[0])
         shape = x.shape
         x2 = x.reshape(-1, shape[-1])
@@ -332,10 +340,11 @@ class DoubleStreamBlock(torch.nn.Module):
         _heads_into(self.img_attn, _linear(self.img_attn.qkv, _adaln(img, i_sh1, i_sc1)), cos, sin, q, k, v, n_txt)
         o = _sdpa_heads(q, k, v)
         img = _residual(img, i_g1, _linear(self.img_attn.proj, _heads_staged(o, n_txt, n_img)))
-        h = _linear(self.img_mlp[0], _adaln(img, i_sh2, i_sc2), gelu=True)
+        # fc1 writes its GELU output straight as fc2's fp16 operand (no staging pass between them)
+        h = _linear(self.img_mlp[0], _adaln(img, i_sh2, i_sc2), gelu=True, staged_out=True)
         img = _residual(img, i_g2, _linear(self.img_mlp[2], h), inplace=True)
         txt = _residual(txt, t_g1, _linear(self.txt_attn.proj, _heads_staged(o, 0, n_txt)))
-        h = _linear(self.txt_mlp[0], _adaln(txt, t_sh2, t_sc2), gelu=True)
+        h = _linear(self.txt_mlp[0], _adaln(txt, t_sh2, t_sc2), gelu=True, staged_out=True)
         txt = _residual(txt, t_g2, _linear(self.txt_mlp[2], h), inplace=True)
         return img, txt
 

@@ -80,6 +80,19 @@ int qlinear_abi_version(void);
  * Linear -> nn.GELU(approximate="tanh") of the DiT MLP, in one kernel (no counterpart in the
  * reference's extension, whose GELU is a separate torch op). */
 #define QL_W4A16_GELU_TANH 2
+/* flags bit: store the output as the next GEMM's row-scaled fp16 operand instead of bfloat16.
+ * Each value is computed exactly as for out_dtype QL_BF16 (GELU included) and rounded to bf16,
+ * then stored as the fp16 number value * 2^-e_m, exact for every value of row m above 2^-31 of
+ * the row's bound B_m = 2^15 rs_m max_n ||W_n||_1 (1 + 1e-4) + max|bias| + 0.17 (rs_m = the input
+ * row factor: max |x[m, :]| < 2^15 rs_m; 0.17 bounds GELU's negative lobe), with 2^-e_m B_m in
+ * [2^14, 2^15) so nothing overflows; out_row_scale[m] = 2^e_m. Pass y (fp16 [M, N]) and
+ * out_row_scale to the next qlinear_w4a16_gemm as x (QL_F16) and row_scale: the bf16 activation
+ * between two linears without the staging pass. out_dtype must be QL_BF16 (the logical dtype),
+ * bias bfloat16; x float16 with row_scale, or bfloat16 / float32 x on the fp16 route; out_bound
+ * from qlinear_w4a16_out_bound for this w_q4 / w_scale / bias. Tile kernels 0-3 and 5 only (the
+ * automatic plan never picks another). No counterpart in the reference, whose linears each read
+ * and write their activations. */
+#define QL_W4A16_F16_ROWSCALED 4
 /* flags bits 8-11: 0 = automatic kernel choice, c + 1 = force kernel configuration c
  * (0-3: 256 / 128 / 64 / 16-row x 256-column tiles, 4 waves; 4-6: 256 x 256 tiles with 8 waves
  * as 2 x 4, 8 waves as 1 x 8, 4 waves as 1 x 4, K % 64 == 0, whole tiles only; 7: M <= 4,
@@ -97,8 +110,17 @@ size_t qlinear_w4a16_workspace_bytes(int x_dtype, int64_t M, int64_t N, int64_t 
 
 int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const float* row_scale,
                        const void* w_q4, const float* w_scale, const float* col_scale,
-                       const void* bias, void* y, int64_t M, int64_t N, int64_t K, int splits,
-                       int flags, void* workspace, size_t workspace_bytes, void* stream);
+                       const void* bias, void* y, const float* out_bound, float* out_row_scale,
+                       int64_t M, int64_t N, int64_t K, int splits, int flags, void* workspace,
+                       size_t workspace_bytes, void* stream);
+
+/* The weight's output bound for QL_W4A16_F16_ROWSCALED: bound[0] = max_n sum_k |dequant W_nk| *
+ * (1 + 2^-10), bound[1] = max_n |bias_n| (0 when bias is NULL). bound holds
+ * QL_W4A16_OUT_BOUND_FLOATS(N) floats (the rest is scratch of the two-pass reduction). Depends
+ * only on w_q4, w_scale and bias: compute once per weight. */
+#define QL_W4A16_OUT_BOUND_FLOATS(N) (2 + ((N) + 3) / 4)
+int qlinear_w4a16_out_bound(const void* w_q4, const float* w_scale, const void* bias, int bias_dtype,
+                            int64_t N, int64_t K, float* bound, void* stream);
 
 /* Allocation-free variant of qlinear_w4a16_gemm, with the same arguments, checks and results
  * minus the workspace. No counterpart in the reference: it is for callers that cannot allocate
@@ -113,8 +135,9 @@ int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const float* r
 #define QL_W4A16_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
 int qlinear_w4a16_gemm_noalloc(int x_dtype, int out_dtype, const void* x, const float* row_scale,
                                const void* w_q4, const float* w_scale, const float* col_scale,
-                               const void* bias, void* y, int64_t M, int64_t N, int64_t K,
-                               int splits, int flags, void* stream);
+                               const void* bias, void* y, const float* out_bound,
+                               float* out_row_scale, int64_t M, int64_t N, int64_t K, int splits,
+                               int flags, void* stream);
 
 /* Column factors of the fp16 dequant: col_scale[n] = 2^e_n with 8 * max_g |w_scale[n, g]| * 2^-e_n
  * in [2^14, 2^15) (e_n clamped to [-126, 126]; 1 for a column whose scales are all 0 or not

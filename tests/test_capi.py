@@ -39,7 +39,7 @@ def lib():
 def test_header_parses():
     fns = _header_functions()
     assert {"qlinear_w4a16_gemm", "qlinear_w8a8_gemm", "qlinear_quantize_int4", "qlinear_last_error"} <= set(fns)
-    assert fns["qlinear_w4a16_gemm"] == 17 and fns["qlinear_abi_version"] == 0
+    assert fns["qlinear_w4a16_gemm"] == 19 and fns["qlinear_abi_version"] == 0
 
 
 def test_every_declared_symbol_is_exported(lib):
@@ -72,47 +72,47 @@ def _err(lib):
 def test_w4a16_argument_checks(lib):
     f = lib.qlinear_w4a16_gemm
     # bad activation dtype (int32)
-    assert f(3, 0, None, None, None, None, None, None, None, 4, 64, 64, 0, 0, None, 0, None) == QL_ERR_DTYPE
+    assert f(3, 0, None, None, None, None, None, None, None, None, None, 4, 64, 64, 0, 0, None, 0, None) == QL_ERR_DTYPE
     assert "x dtype" in _err(lib)
-    assert f(2, 3, None, None, None, None, None, None, None, 4, 64, 64, 0, 0, None, 0, None) == QL_ERR_DTYPE
+    assert f(2, 3, None, None, None, None, None, None, None, None, None, 4, 64, 64, 0, 0, None, 0, None) == QL_ERR_DTYPE
     # K not a multiple of the 32-wide group
-    assert f(2, 2, None, None, None, None, None, None, None, 4, 64, 48, 0, 0, None, 0, None) == QL_ERR_SHAPE
+    assert f(2, 2, None, None, None, None, None, None, None, None, None, 4, 64, 48, 0, 0, None, 0, None) == QL_ERR_SHAPE
     assert "K % 32 == 0" in _err(lib) and "K=48" in _err(lib)
-    assert f(2, 2, None, None, None, None, None, None, None, 4, 0, 64, 0, 0, None, 0, None) == QL_ERR_SHAPE
-    assert f(2, 2, None, None, None, None, None, None, None, 4, 64, 64, 65, 0, None, 0, None) == QL_ERR_ARG
-    assert f(2, 2, None, None, None, None, None, None, None, 4, 64, 64, 0, 4, None, 0, None) == QL_ERR_ARG
+    assert f(2, 2, None, None, None, None, None, None, None, None, None, 4, 0, 64, 0, 0, None, 0, None) == QL_ERR_SHAPE
+    assert f(2, 2, None, None, None, None, None, None, None, None, None, 4, 64, 64, 65, 0, None, 0, None) == QL_ERR_ARG
+    assert f(2, 2, None, None, None, None, None, None, None, None, None, 4, 64, 64, 0, 4, None, 0, None) == QL_ERR_ARG
     # row scales are only meaningful for fp16 activations staged by qlinear_rows_to_f16
-    assert f(2, 2, None, ctypes.c_void_p(16), None, None, None, None, None, 4, 64, 64, 0, 0, None, 0, None) == QL_ERR_ARG
+    assert f(2, 2, None, ctypes.c_void_p(16), None, None, None, None, None, None, None, 4, 64, 64, 0, 0, None, 0, None) == QL_ERR_ARG
     # M == 0 is a no-op that succeeds (binding.cpp:64, 93 of the reference return empty outputs)
-    assert f(2, 2, None, None, None, None, None, None, None, 0, 64, 64, 0, 0, None, 0, None) == QL_OK
-    assert f(2, 2, None, None, None, None, None, None, None, 4, 64, 64, 0, 0, None, 0, None) == QL_ERR_ARG
+    assert f(2, 2, None, None, None, None, None, None, None, None, None, 0, 64, 64, 0, 0, None, 0, None) == QL_OK
+    assert f(2, 2, None, None, None, None, None, None, None, None, None, 4, 64, 64, 0, 0, None, 0, None) == QL_ERR_ARG
     assert "null" in _err(lib)
-    assert f(1, 2, ctypes.c_void_p(8), None, ctypes.c_void_p(16), ctypes.c_void_p(16), None, None, ctypes.c_void_p(16),
+    assert f(1, 2, ctypes.c_void_p(8), None, ctypes.c_void_p(16), ctypes.c_void_p(16), None, None, ctypes.c_void_p(16), None, None,
              4, 64, 64, 0, 0, None, 0, None) == QL_ERR_ALIGN
     # forced kernel configurations (flags bits 8-11 = configuration + 1): 0-8 exist; the 256 x 256
     # configurations 4-6 need K % 64 == 0 and whole tiles
     cfg = lambda c: (c + 1) << 8  # noqa: E731
-    assert f(2, 2, None, None, None, None, None, None, None, 0, 64, 64, 0, cfg(9), None, 0, None) == QL_ERR_ARG
+    assert f(2, 2, None, None, None, None, None, None, None, None, None, 0, 64, 64, 0, cfg(9), None, 0, None) == QL_ERR_ARG
     assert "configuration 9 does not exist" in _err(lib)
     # configuration 8 (MFMA, M <= 16): 16-bit x, K % 128 == 0, K <= 4096, no K split
-    assert f(2, 2, None, None, None, None, None, None, None, 0, 64, 128, 0, cfg(8), None, 0, None) == QL_OK
-    assert f(0, 2, None, None, None, None, None, None, None, 0, 64, 128, 0, cfg(8), None, 0, None) == QL_ERR_SHAPE
-    assert f(2, 2, None, None, None, None, None, None, None, 17, 64, 128, 0, cfg(8), None, 0, None) == QL_ERR_SHAPE
-    assert f(2, 2, None, None, None, None, None, None, None, 1, 64, 96, 0, cfg(8), None, 0, None) == QL_ERR_SHAPE
-    assert f(2, 2, None, None, None, None, None, None, None, 1, 64, 4224, 0, cfg(8), None, 0, None) == QL_ERR_SHAPE
+    assert f(2, 2, None, None, None, None, None, None, None, None, None, 0, 64, 128, 0, cfg(8), None, 0, None) == QL_OK
+    assert f(0, 2, None, None, None, None, None, None, None, None, None, 0, 64, 128, 0, cfg(8), None, 0, None) == QL_ERR_SHAPE
+    assert f(2, 2, None, None, None, None, None, None, None, None, None, 17, 64, 128, 0, cfg(8), None, 0, None) == QL_ERR_SHAPE
+    assert f(2, 2, None, None, None, None, None, None, None, None, None, 1, 64, 96, 0, cfg(8), None, 0, None) == QL_ERR_SHAPE
+    assert f(2, 2, None, None, None, None, None, None, None, None, None, 1, 64, 4224, 0, cfg(8), None, 0, None) == QL_ERR_SHAPE
     assert "K % 128 == 0" in _err(lib)
-    assert f(2, 2, None, None, None, None, None, None, None, 0, 64, 128, 2, cfg(8), None, 0, None) == QL_ERR_ARG
+    assert f(2, 2, None, None, None, None, None, None, None, None, None, 0, 64, 128, 2, cfg(8), None, 0, None) == QL_ERR_ARG
     assert "no K split" in _err(lib)
     # configuration 7 (VALU, M <= 4): 16-bit x, K <= 8192
-    assert f(0, 2, None, None, None, None, None, None, None, 0, 64, 64, 0, cfg(7), None, 0, None) == QL_ERR_SHAPE
-    assert f(2, 2, None, None, None, None, None, None, None, 5, 64, 64, 0, cfg(7), None, 0, None) == QL_ERR_SHAPE
-    assert f(2, 2, None, None, None, None, None, None, None, 1, 64, 8224, 0, cfg(7), None, 0, None) == QL_ERR_SHAPE
+    assert f(0, 2, None, None, None, None, None, None, None, None, None, 0, 64, 64, 0, cfg(7), None, 0, None) == QL_ERR_SHAPE
+    assert f(2, 2, None, None, None, None, None, None, None, None, None, 5, 64, 64, 0, cfg(7), None, 0, None) == QL_ERR_SHAPE
+    assert f(2, 2, None, None, None, None, None, None, None, None, None, 1, 64, 8224, 0, cfg(7), None, 0, None) == QL_ERR_SHAPE
     for c in range(8):
-        assert f(2, 2, None, None, None, None, None, None, None, 0, 64, 64, 0, cfg(c), None, 0, None) == QL_OK
+        assert f(2, 2, None, None, None, None, None, None, None, None, None, 0, 64, 64, 0, cfg(c), None, 0, None) == QL_OK
     for c in (4, 5, 6):
-        assert f(2, 2, None, None, None, None, None, None, None, 0, 64, 96, 0, cfg(c), None, 0, None) == QL_ERR_SHAPE
+        assert f(2, 2, None, None, None, None, None, None, None, None, None, 0, 64, 96, 0, cfg(c), None, 0, None) == QL_ERR_SHAPE
         assert "K % 64 == 0" in _err(lib)
-        assert f(2, 2, None, None, None, None, None, None, None, 0, 64, 128, 2, cfg(c), None, 0, None) == QL_ERR_ARG
+        assert f(2, 2, None, None, None, None, None, None, None, None, None, 0, 64, 128, 2, cfg(c), None, 0, None) == QL_ERR_ARG
         assert "whole tiles" in _err(lib)
 
 
