@@ -145,10 +145,11 @@ def main():
             e0 = torch.cuda.Event(enable_timing=True)
             e1 = torch.cuda.Event(enable_timing=True)
             e0.record()
-        # the fp16 dequant's column factors and the output bound are computed once per weight and
-        # kept with it (as the node's Linear does), not per call
+        # the fp16 dequant's column factors, the group-major scale copy and the output bound are
+        # computed once per weight and kept with it (as the node's Linear does), not per call
         y = _lib.w4a16_gemm(a16, wq, ws, bias, out_dtype=torch.bfloat16, row_scale=rs, gelu=gelu,
-                            col_scale=_lib.cached_col_scales(ws), f16_rowscaled=rowscaled,
+                            col_scale=_lib.cached_col_scales(ws), scales_kn=_lib.cached_scales_kn(ws),
+                            f16_rowscaled=rowscaled,
                             out_bound=_lib.cached_out_bound(wq, ws, bias) if rowscaled else None)
         if record:
             e1.record()
@@ -340,17 +341,18 @@ def bench_c4(args):
         for _ in range(12):
             w = torch.randn(N, K, device="cuda", generator=g) * 0.02
             q, s = ops.quantize_pack_int4(w)
-            ws.append((q, s, _lib.w4a16_col_scales(s)))  # kept with the weight, as the node's Linear does
+            # column factors and group-major scales kept with the weight, as the node's Linear does
+            ws.append((q, s, _lib.w4a16_col_scales(s), _lib.w4a16_scales_kn(s)))
         del w
         with torch.cuda.stream(side):
-            for q, s, c in ws:  # eager calls on the capture stream first: its workspace exists before capture
-                y = _lib.w4a16_gemm(x, q, s, b, out_dtype=torch.bfloat16, col_scale=c)
+            for q, s, c, kn in ws:  # eager calls on the capture stream first: its workspace exists before capture
+                y = _lib.w4a16_gemm(x, q, s, b, out_dtype=torch.bfloat16, col_scale=c, scales_kn=kn)
         side.synchronize()
         graph = torch.cuda.CUDAGraph()
         with torch.cuda.graph(graph, stream=side):
             for i in range(48):
-                q, s, c = ws[i % 12]
-                y = _lib.w4a16_gemm(x, q, s, b, out_dtype=torch.bfloat16, col_scale=c)
+                q, s, c, kn = ws[i % 12]
+                y = _lib.w4a16_gemm(x, q, s, b, out_dtype=torch.bfloat16, col_scale=c, scales_kn=kn)
         graph.replay()
         torch.cuda.synchronize()
         times = []

@@ -47,11 +47,12 @@ SIGNATURES = {
     "qlinear_abi_version": (_c_int, []),
     "qlinear_w4a16_workspace_bytes": (_c_size_t, [_c_int, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int]),
     "qlinear_w4a16_gemm": (_c_int, [_c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
-                                    _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_vp, _c_size_t, _c_vp]),
+                                    _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_vp, _c_size_t, _c_vp]),
+    "qlinear_w4a16_scales_kn": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
     "qlinear_w4a16_col_scales": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
     "qlinear_w4a16_out_bound": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_i64, _c_i64, _c_vp, _c_vp]),
     "qlinear_w4a16_gemm_noalloc": (_c_int, [_c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
-                                            _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_vp]),
+                                            _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_vp]),
     "qlinear_rows_to_f16": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
     "qlinear_w4a16_auto_splits": (_c_int, [_c_i64, _c_i64, _c_i64, _c_int]),
     "qlinear_quantize_int4": (_c_int, [_c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
@@ -175,6 +176,43 @@ def w4a16_col_scales(w_scale: torch.Tensor) -> torch.Tensor:
     return cs
 
 
+def w4a16_scales_kn(w_scale: torch.Tensor) -> torch.Tensor:
+    """Group-major copy of the group scales: fp32 [K/32, N] with out[g, n] = w_scale[n, g]
+    (qlinear_w4a16_scales_kn). Passed as w4a16_gemm(..., scales_kn=...), the tile kernels read
+    it in place of w_scale: the same results, fewer memory requests."""
+    lib = load_library()
+    w_scale = _dev_tensor(w_scale, "w_scale")
+    if w_scale.dtype != torch.float32 or w_scale.dim() != 2:
+        raise RuntimeError(f"w_scale must be a float32 [N, K/32] tensor, got {w_scale.dtype} {tuple(w_scale.shape)}")
+    N, G = w_scale.shape
+    out = torch.empty((G, N), dtype=torch.float32, device=w_scale.device)
+    with torch.cuda.device(w_scale.device):
+        rc = lib.qlinear_w4a16_scales_kn(w_scale.contiguous().data_ptr(), out.data_ptr(), N, G * 32,
+                                         _stream_ptr(w_scale.device))
+    _check(rc, "w4a16_scales_kn")
+    return out
+
+
+def cached_scales_kn(w_scale: torch.Tensor) -> torch.Tensor | None:
+    """w4a16_scales_kn(w_scale), kept on the w_scale tensor object and recomputed when the tensor
+    is modified in place (version counter) or used from another stream; None for tensors without
+    a version counter (inference-mode tensors), for which the GEMM reads w_scale itself."""
+    try:
+        version = w_scale._version
+    except RuntimeError:
+        return None
+    stream = _stream_ptr(w_scale.device)
+    hit = getattr(w_scale, "_qlinear_scales_kn", None)
+    if hit is not None and hit[0] == version and hit[1] == stream:
+        return hit[2]
+    kn = w4a16_scales_kn(w_scale)
+    try:
+        w_scale._qlinear_scales_kn = (version, stream, kn)
+    except (AttributeError, RuntimeError):
+        pass
+    return kn
+
+
 def w4a16_out_bound(w_q4: torch.Tensor, w_scale: torch.Tensor, bias: torch.Tensor | None = None) -> torch.Tensor:
     """{max_n ||dequant W_n||_1 (1 + 2^-10), max_n |bias_n|} (fp32 [2] on the weight's device): the
     bound the row-scaled fp16 output (w4a16_gemm(..., f16_rowscaled=True)) derives its row factors
@@ -244,7 +282,8 @@ def w4a16_gemm(x: torch.Tensor, w_q4: torch.Tensor, w_scale: torch.Tensor, bias:
                out_dtype: torch.dtype | None = None, splits: int = 0, bf16_mfma: bool = False,
                row_scale: torch.Tensor | None = None, config: int | None = None,
                gelu: bool = False, col_scale: torch.Tensor | None = None, noalloc: bool = False,
-               f16_rowscaled: bool = False, out_bound: torch.Tensor | None = None):
+               f16_rowscaled: bool = False, out_bound: torch.Tensor | None = None,
+               scales_kn: torch.Tensor | None = None):
     """y[M, N] = x[M, K] @ dequant(w_q4, w_scale)^T (+ bias) on the gfx950 W4A16 kernel.
     x: fp16/bf16/fp32 [M, K]; w_q4: int8 [N, K/2]; w_scale: fp32 [N, K/32]; bias: out_dtype [N].
     bf16 and fp32 activations go through the exact row-scaled fp16 staging unless bf16_mfma is
@@ -258,7 +297,8 @@ def w4a16_gemm(x: torch.Tensor, w_q4: torch.Tensor, w_scale: torch.Tensor, bias:
     from torch's allocator; calls needing more than QL_W4A16_NOALLOC_SCRATCH_BYTES raise).
     f16_rowscaled: the bf16 result (out_dtype must be bfloat16) stored as the next GEMM's row-scaled
     fp16 operand (QL_W4A16_F16_ROWSCALED); returns (y16 fp16 [M, N], row_scale fp32 [M]) to pass on
-    as (x, row_scale). out_bound: w4a16_out_bound of this weight and bias (computed when None)."""
+    as (x, row_scale). out_bound: w4a16_out_bound of this weight and bias (computed when None).
+    scales_kn: w4a16_scales_kn of this w_scale (group-major, read by the tile kernels), or None."""
     lib = load_library()
     x = _dev_tensor(x, "x")
     w_q4 = _dev_tensor(w_q4, "w_q4")
@@ -309,12 +349,18 @@ def w4a16_gemm(x: torch.Tensor, w_q4: torch.Tensor, w_scale: torch.Tensor, bias:
         if col_scale.dtype != torch.float32 or col_scale.numel() != N or col_scale.device != x.device:
             raise RuntimeError(f"col_scale must be a float32 [{N}] tensor on {x.device}, got {col_scale.dtype} "
                                f"{tuple(col_scale.shape)} on {col_scale.device}")
+    if scales_kn is not None:
+        scales_kn = _dev_tensor(scales_kn, "scales_kn")
+        if scales_kn.dtype != torch.float32 or tuple(scales_kn.shape) != (K // 32, N) or scales_kn.device != x.device:
+            raise RuntimeError(f"scales_kn must be a float32 [{K // 32}, {N}] tensor on {x.device}, got "
+                               f"{scales_kn.dtype} {tuple(scales_kn.shape)} on {scales_kn.device}")
+    kn_ptr = scales_kn.data_ptr() if scales_kn is not None else None
     with torch.cuda.device(x.device):
         stream = _stream_ptr(x.device)
         if noalloc:
             rc = lib.qlinear_w4a16_gemm_noalloc(xdt, _DTYPE_CODE[out_dtype], x.data_ptr(),
                                                 row_scale.data_ptr() if row_scale is not None else None,
-                                                w_q4.data_ptr(), w_scale.data_ptr(),
+                                                w_q4.data_ptr(), w_scale.data_ptr(), kn_ptr,
                                                 col_scale.data_ptr() if col_scale is not None else None,
                                                 bias.data_ptr() if bias is not None else None, y.data_ptr(),
                                                 out_bound.data_ptr() if out_bound is not None else None,
@@ -326,7 +372,7 @@ def w4a16_gemm(x: torch.Tensor, w_q4: torch.Tensor, w_scale: torch.Tensor, bias:
         ws = _workspaces.get(x.device, stream, nbytes) if nbytes else None
         rc = lib.qlinear_w4a16_gemm(xdt, _DTYPE_CODE[out_dtype], x.data_ptr(),
                                     row_scale.data_ptr() if row_scale is not None else None,
-                                    w_q4.data_ptr(), w_scale.data_ptr(),
+                                    w_q4.data_ptr(), w_scale.data_ptr(), kn_ptr,
                                     col_scale.data_ptr() if col_scale is not None else None,
                                     bias.data_ptr() if bias is not None else None, y.data_ptr(),
                                     out_bound.data_ptr() if out_bound is not None else None,

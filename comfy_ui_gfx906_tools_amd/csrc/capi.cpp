@@ -106,6 +106,18 @@ int64_t tile256_whole(int64_t tiles, int cus) {
   return (rem > 0 && 2 * rem <= cus) ? tiles - rem : tiles;
 }
 
+// K pieces per tile of the 256-column kernel, variant 1 only: an explicit splits >= 2, or (splits
+// 0) enough pieces to give every CU one when the tiles alone fill fewer than half of them, each
+// piece at least kMinPieceStages stages of 64 K long (shorter ones spend more on the pipeline's
+// fill and the partial round trip than they gain).
+constexpr int kMinPieceStages = 4;
+int tile256_pieces(int tiles, int stages, int splits, int cfg, int cus) {
+  if (cfg != kCfgTile256Auto || splits == 1) return 1;
+  if (splits >= 2) return std::min(splits, stages);
+  if (2 * tiles > cus) return 1;
+  return std::max(1, std::min(cus / tiles, stages / kMinPieceStages));
+}
+
 // 256 x 256 tiles once there are at least a quarter as many as CUs. Measured on MI355X (bf16 x via
 // the fp16 staging, Flux DiT shapes): the 128-row kernel spends 1.6-2.2x the time per flop, so the
 // 256 x 256 kernel wins even with most CUs idle (M=4096 N=3072 K=3072, 192 tiles: 80 vs 128 us;
@@ -158,6 +170,9 @@ int w4a16_cfg_for(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, int 
   if (exact_ok && skinny_fits(x_dtype, M, N, K)) return kCfgSkinny;
   if (exact_ok && gemv_fits(x_dtype, M, K)) return kCfgGemv;
   if (M <= 16) return 3;
+  // 17-256 rows: the 4-wave kernel's 64- / 128-row tiles with K pieces. (The 256-column kernel's
+  // 64- / 128-row tiles, configuration 5 forced, measured no faster with the weights streamed
+  // from HBM: K = 4096, N = 10240, M = 64 28.7 vs 27.4 us, M = 128 35.4 vs 35.3 us.)
   if (M <= 64) return 2;
   if (M <= 128) return 1;
   return (splits < 2 && prefer_tile256(M, N, K, cus)) ? kCfgTile256Auto : 1;
@@ -181,7 +196,9 @@ W4A16Plan plan_w4a16(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, i
     pl.BN = 16 * skinny_blocks(M, N, cus);
     pl.stages = 1;
   } else if (is_tile256(pl.cfg)) {
-    pl.BM = pl.BN = 256;
+    // variant 1 (configuration 5) takes the shortest tile height that covers M, 64 / 128 / 256
+    pl.BM = pl.cfg != kCfgTile256Auto ? 256 : M <= 64 ? 64 : M <= 128 ? 128 : 256;
+    pl.BN = 256;
     pl.stages = (int)(K / 64);
   } else {
     const W4A16Config& c = w4a16_config(pl.cfg);
@@ -197,7 +214,13 @@ W4A16Plan plan_w4a16(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, i
   if (direct) {
     // one launch, no K split across workgroups
   } else if (is_tile256(pl.cfg)) {
-    pl.dp_tiles = splits == 1 ? tiles : (int)tile256_whole(tiles, cus);
+    const int k = tile256_pieces(tiles, pl.stages, splits, pl.cfg, cus);
+    if (k > 1) {  // every tile cut into k K pieces (variant 1)
+      pl.dp_tiles = 0;
+      pl.ksplit = k;
+    } else {
+      pl.dp_tiles = (splits == 1 || pl.BM != 256) ? tiles : (int)tile256_whole(tiles, cus);
+    }
   } else if (splits >= 2 && tiles <= kMaxCutTiles) {
     pl.ksplit = std::min(splits, pl.stages);
     if (pl.ksplit >= 2) pl.dp_tiles = 0;
@@ -223,7 +246,7 @@ W4A16Plan plan_w4a16(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, i
     }
   }
   pl.grid = pl.dp_tiles + (tiles - pl.dp_tiles) * pl.ksplit;
-  const size_t partial_bytes = (pl.dp_tiles < tiles && !is_tile256(pl.cfg) && !direct)
+  const size_t partial_bytes = (pl.dp_tiles < tiles && !direct && (!is_tile256(pl.cfg) || pl.ksplit > 1))
                                    ? (size_t)(tiles - pl.dp_tiles) * pl.ksplit * pl.BM * pl.BN * sizeof(float)
                                    : 0;
   pl.off_row_scale = 0;
@@ -276,7 +299,7 @@ int check_w4a16_args(int x_dtype, int out_dtype, const float* row_scale, int64_t
                                            forced - 1, kCfgLast);
     if (forced && is_tile256(forced - 1) && K % 64 != 0)
       return fail(QL_ERR_SHAPE, "kernel configuration %d needs K %% 64 == 0, got K=%lld", forced - 1, (long long)K);
-    if (forced && is_tile256(forced - 1) && splits >= 2)
+    if (forced && is_tile256(forced - 1) && forced - 1 != kCfgTile256Auto && splits >= 2)
       return fail(QL_ERR_ARG, "kernel configuration %d runs whole tiles only (splits 0 or 1), got splits=%d",
                   forced - 1, splits);
     if (forced == kCfgGemv + 1 && !gemv_fits(x_dtype, M, K))
@@ -354,7 +377,7 @@ extern "C" {
 
 const char* qlinear_last_error(void) { return g_last_error.c_str(); }
 
-int qlinear_abi_version(void) { return (2 << 16) | 0; }
+int qlinear_abi_version(void) { return (3 << 16) | 0; }
 
 size_t qlinear_w4a16_workspace_bytes(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, int flags,
                                      int device) {
@@ -375,7 +398,8 @@ int qlinear_w4a16_auto_splits(int64_t M, int64_t N, int64_t K, int device) {
 }
 
 int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const float* row_scale, const void* w_q4,
-                       const float* w_scale, const float* col_scale, const void* bias, void* y, const float* out_bound,
+                       const float* w_scale, const float* w_scale_kn, const float* col_scale, const void* bias, void* y,
+                       const float* out_bound,
                        float* out_row_scale, int64_t M, int64_t N, int64_t K, int splits, int flags, void* workspace,
                        size_t workspace_bytes, void* stream) {
   if (int rc = check_w4a16_args(x_dtype, out_dtype, row_scale, M, N, K, splits, flags)) return rc;
@@ -417,7 +441,11 @@ int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const float* r
     p.row_scale = rs;
   }
   p.wq = w_q4;
-  p.ws = w_scale;
+  // the tile kernels read the group-major copy when given; the direct kernels (7, 8) read whole
+  // column rows of w_scale, which that layout already serves in long runs
+  const bool kn = w_scale_kn && pl.cfg != kCfgGemv && pl.cfg != kCfgSkinny;
+  p.ws = kn ? w_scale_kn : w_scale;
+  p.scales_kn = kn ? 1 : 0;
   p.bias = bias;
   p.y = y;
   p.partial = pl.total ? (float*)(ws + pl.off_partial) : nullptr;
@@ -434,6 +462,7 @@ int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const float* r
   p.stages = pl.stages;
   p.dp_tiles = pl.dp_tiles;
   p.ksplit = pl.ksplit;
+  p.tile_rows = pl.BM;
   const bool bf16_mfma = x_dtype == QL_BF16 && !pl.prepass;
   const hipError_t e = pl.cfg == kCfgGemv     ? w4a16_gemv_launch(x_dtype == QL_BF16, p, (hipStream_t)stream)
                        : pl.cfg == kCfgSkinny ? w4a16_skinny_launch(x_dtype == QL_BF16, pl.BN / 16, p, (hipStream_t)stream)
@@ -445,7 +474,8 @@ int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const float* r
 }
 
 int qlinear_w4a16_gemm_noalloc(int x_dtype, int out_dtype, const void* x, const float* row_scale, const void* w_q4,
-                               const float* w_scale, const float* col_scale, const void* bias, void* y,
+                               const float* w_scale, const float* w_scale_kn, const float* col_scale, const void* bias,
+                               void* y,
                                const float* out_bound, float* out_row_scale, int64_t M, int64_t N, int64_t K,
                                int splits, int flags, void* stream) {
   // the checks qlinear_w4a16_gemm makes before planning, so the size check below sees a valid plan
@@ -463,7 +493,7 @@ int qlinear_w4a16_gemm_noalloc(int x_dtype, int out_dtype, const void* x, const 
   if (need > 0) {
     if (int rc = scratch_address(&ws)) return rc;
   }
-  return qlinear_w4a16_gemm(x_dtype, out_dtype, x, row_scale, w_q4, w_scale, col_scale, bias, y, out_bound,
+  return qlinear_w4a16_gemm(x_dtype, out_dtype, x, row_scale, w_q4, w_scale, w_scale_kn, col_scale, bias, y, out_bound,
                             out_row_scale, M, N, K, splits, flags, ws, need > 0 ? kNoAllocScratchBytes : 0, stream);
 }
 
@@ -539,6 +569,28 @@ int qlinear_check_launch_plan(int op, int x_dtype, int64_t M, int64_t N, int64_t
       return QL_OK;
     }
     if (pl.dp_tiles < 0 || pl.dp_tiles > tiles) return fail(QL_ERR_SHAPE, "dp_tiles %d of %d", pl.dp_tiles, tiles);
+    if (is_tile256(pl.cfg) && (pl.BM != 256 || pl.ksplit > 1)) {
+      // variant 1 with BM-row tiles: all whole, or all cut into ksplit K pieces (partials + reduce)
+      if (pl.cfg != kCfgTile256Auto || (pl.BM != 64 && pl.BM != 128 && pl.BM != 256))
+        return fail(QL_ERR_SHAPE, "tile256 rows: configuration %d with %d-row tiles", pl.cfg, pl.BM);
+      if (pl.ksplit > 1 && pl.dp_tiles != 0)
+        return fail(QL_ERR_SHAPE, "tile256 rows: %d whole tiles beside K pieces", pl.dp_tiles);
+      if (pl.ksplit < 1 || pl.ksplit > pl.stages)
+        return fail(QL_ERR_SHAPE, "tile256 rows: ksplit %d outside [1, %d stages]", pl.ksplit, pl.stages);
+      fresh(pl.tiles_m, pl.tiles_n, pl.ksplit);
+      if (int rc = launch("tile256 rows whole", pl.dp_tiles, 0, 1, 1, pl.BM, 256, kTile256GroupM, false)) return rc;
+      if (int rc = launch("tile256 rows cut", (tiles - pl.dp_tiles) * pl.ksplit, pl.dp_tiles, 1, pl.ksplit, pl.BM, 256,
+                          kTile256GroupM, false))
+        return rc;
+      if (pl.ksplit > 1) {
+        const size_t partial_slots =
+            pl.total >= pl.off_partial ? (pl.total - pl.off_partial) / ((size_t)pl.BM * pl.BN * 4) : 0;
+        if (partial_slots < (size_t)tiles * pl.ksplit)
+          return fail(QL_ERR_SHAPE, "tile256 rows: workspace holds %zu partial tiles, the launch writes %d",
+                      partial_slots, tiles * pl.ksplit);
+      }
+      return all_seen("tile256 rows");
+    }
     if (is_tile256(pl.cfg)) {
       // whole 256 x 256 tiles, then the rest as 128-row halves (a half wholly past M exits early)
       fresh(pl.tiles_m, pl.tiles_n, 2);
@@ -629,6 +681,17 @@ int qlinear_w4a16_col_scales(const float* w_scale, float* col_scale, int64_t N, 
   if (!w_scale || !col_scale) return fail(QL_ERR_ARG, "null w_scale / col_scale pointer");
   const hipError_t e = col_scales_launch(w_scale, col_scale, N, K / 32, (hipStream_t)stream);
   if (e != hipSuccess) return fail(QL_ERR_LAUNCH, "col_scales launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
+int qlinear_w4a16_scales_kn(const float* w_scale, float* w_scale_kn, int64_t N, int64_t K, void* stream) {
+  if (N < 0 || K < 32 || K % 32 != 0 || N > INT32_MAX / 2 || K > (1 << 22) || N * (K / 32) > INT32_MAX / 4)
+    return fail(QL_ERR_SHAPE, "expected w_scale [N, K/32] with K %% 32 == 0, 32 <= K <= 4194304, N * K / 8 < 2^31; "
+                "got N=%lld K=%lld", (long long)N, (long long)K);
+  if (N == 0) return ok();
+  if (!w_scale || !w_scale_kn) return fail(QL_ERR_ARG, "null w_scale / w_scale_kn pointer");
+  const hipError_t e = scales_kn_launch(w_scale, w_scale_kn, N, K / 32, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(QL_ERR_LAUNCH, "scales_kn launch failed: %s", hipGetErrorString(e));
   return ok();
 }
 

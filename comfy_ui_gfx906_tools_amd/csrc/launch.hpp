@@ -20,7 +20,7 @@ constexpr int kW8A8T256GroupM = 4;  // w8a8_tile256.hip
 struct W4A16Params {
   const void* x;         // [M, K] bf16 / fp16
   const void* wq;        // [N, K/2] packed int4
-  const float* ws;       // [N, K/32]
+  const float* ws;       // [N, K/32], or [K/32, N] (group-major) when scales_kn
   const void* bias;      // [N] out dtype, or null
   void* y;               // [M, N] out dtype
   const float* row_scale;  // [M] power-of-two factor applied in the epilogue, or null
@@ -41,6 +41,8 @@ struct W4A16Params {
   int dp_tiles;          // tiles processed whole, one workgroup each
   int ksplit;            // K pieces of every tile past dp_tiles (>= 2 when any)
   int tile_base;         // 256 x 256 kernel: first tile of the launch (set by the launcher)
+  int tile_rows;         // 256-column kernel, variant 1: tile height 64, 128 or 256
+  int scales_kn;         // ws is group-major [K/32, N] (qlinear_w4a16_scales_kn)
   int cus;               // compute units of the device (grid sizing)
 };
 
@@ -71,8 +73,13 @@ constexpr int kSkinnyMaxM = 16, kSkinnyMaxK = 4096, kSkinnyMaxBlocks = 3;
 hipError_t w4a16_skinny_launch(bool bf16, int blocks, const W4A16Params& p, hipStream_t stream);
 hipError_t rows_to_scaled_f16_launch(int dtype, const void* x, void* x16, float* row_scale, int64_t M,
                                      int64_t K, hipStream_t stream);
+// Sums the ksplit fp32 partials [BM][BN] of every cut tile (tiles p.dp_tiles .. of the grouped order
+// with group_m tile rows) in piece order and applies the epilogue (w4a16_gemm.hip).
+hipError_t w4a16_reduce_launch(const W4A16Params& p, int BM, int BN, int group_m, hipStream_t stream);
 // col_scale[n] = 2^e_n with 8 max_g |w_scale[n, g]| * 2^-e_n in [2^14, 2^15), e_n clamped to
 // [-126, 126]; 1 for a column whose scales are all zero or not finite (w4a16_gemm.hip).
+// w_scale [N, groups] -> w_scale_kn [groups, N] (group-major copy read by the tile kernels)
+hipError_t scales_kn_launch(const float* w_scale, float* w_scale_kn, int64_t N, int64_t groups, hipStream_t stream);
 hipError_t col_scales_launch(const float* w_scale, float* col_scale, int64_t N, int64_t groups, hipStream_t stream);
 // bound[0] = max_n sum_k |q_nk s_n,k/32| (1 + 2^-10), bound[1] = max_n |bias_n| (0 without bias);
 // bound[2 ..] holds per-workgroup partial maxima, (N + 3) / 4 floats (w4a16_gemm.hip).

@@ -109,7 +109,13 @@ __global__ __launch_bounds__(64 * kWaves) void w4a16_gemm_kernel(W4A16Params p) 
   const int rows = min(M - m0, BM), cols = min(N - n0, BN);
   const rsrc_t rs_a = make_rsrc((const uint16_t*)p.x + (size_t)m0 * K, (uint32_t)rows * K * 2);
   const rsrc_t rs_b = make_rsrc((const uint8_t*)p.wq + (size_t)n0 * (K / 2), (uint32_t)cols * (K / 2));
-  const rsrc_t rs_s = make_rsrc(p.ws + (size_t)n0 * groups, (uint32_t)cols * groups * 4);
+  // scales [N, K/32], or group-major [K/32, N] (scales_kn: a stage's 4 groups of the tile's
+  // columns are 4 runs of BN * 4 bytes instead of BN runs of 16; the range ends at the tile's last
+  // column of the last group row, and a column past N of an earlier row reads a scale of the next
+  // row, which only enters that column's own accumulators, never stored)
+  const int kn = p.scales_kn;
+  const rsrc_t rs_s = kn ? make_rsrc(p.ws + n0, (uint32_t)((groups - 1) * N + cols) * 4)
+                         : make_rsrc(p.ws + (size_t)n0 * groups, (uint32_t)cols * groups * 4);
   // A: wave wn stages rows [wn*BM/4, (wn+1)*BM/4) in kLoadsA loads of 4 rows; load q covers row
   // wn*BM/4 + 4q + j4, whose swizzle depends on q % 4 only
   constexpr int kVoA = kLoadsA < 4 ? kLoadsA : 4;
@@ -121,8 +127,9 @@ __global__ __launch_bounds__(64 * kWaves) void w4a16_gemm_kernel(W4A16Params p) 
   const uint32_t a_q4_step = 16u * K * 2;  // four loads further down = 16 rows
   const int col0 = wn * WN * 16 + r16;
   const uint32_t vo_b = (uint32_t)col0 * (K / 2) + j4 * 16;
-  const uint32_t vo_s = ((uint32_t)col0 * groups + j4) * 4;
-  const uint32_t b_fn_step = 16u * (K / 2), s_fn_step = 16u * groups * 4;
+  const uint32_t vo_s = kn ? ((uint32_t)j4 * N + col0) * 4 : ((uint32_t)col0 * groups + j4) * 4;
+  const uint32_t b_fn_step = 16u * (K / 2), s_fn_step = kn ? 16u * 4 : 16u * groups * 4;
+  const uint32_t s_stage = kn ? (uint32_t)kGroupsPerStage * N * 4 : (uint32_t)kGroupsPerStage * 4;
 
   // Global loads of stage s: B (raw int4 + scales) into registers, then A straight into the LDS
   // buffer `dst`, one vector-memory instruction per call (index l < kLoadsPerStage), so a stage's
@@ -143,7 +150,7 @@ __global__ __launch_bounds__(64 * kWaves) void w4a16_gemm_kernel(W4A16Params p) 
       if (l < WN) {
         raw[l] = buf_load16(live ? rs_b : rs_none, vb, s * 64 + l * b_fn_step);
       } else {
-        sc[l - WN] = buf_load_f32(live ? rs_s : rs_none, vs, s * 16 + (l - WN) * s_fn_step);
+        sc[l - WN] = buf_load_f32(live ? rs_s : rs_none, vs, s * s_stage + (l - WN) * s_fn_step);
       }
     } else {
       const int q = l - 2 * WN;
@@ -420,11 +427,11 @@ __global__ __launch_bounds__(64 * kWaves) void w4a16_gemm_kernel(W4A16Params p) 
 // Sums the ksplit fp32 partials of every cut tile in piece order, applies the row and column
 // scales and the bias, and stores y. Grid: (cut tiles) x (BM*BN / 1024) workgroups of 256 threads, 4 elements
 // per thread.
-__global__ __launch_bounds__(256) void w4a16_reduce_kernel(W4A16Params p, int BM, int BN) {
+__global__ __launch_bounds__(256) void w4a16_reduce_kernel(W4A16Params p, int BM, int BN, int group_m) {
   const int tl = blockIdx.y;  // cut tile index
   const int t = p.dp_tiles + tl;
   int tm, tn;
-  tile_coords(t, p.tiles_m, p.tiles_n, kGroupM, tm, tn);
+  tile_coords(t, p.tiles_m, p.tiles_n, group_m, tm, tn);
   const int idx = (blockIdx.x * 256 + threadIdx.x) * 4;
   if (idx >= BM * BN) return;
   const size_t tile_elems = (size_t)BM * BN;
@@ -599,6 +606,27 @@ __global__ __launch_bounds__(256) void col_scales_kernel(const float* __restrict
   }
 }
 
+// Group-major copy of the scales: kn[g][n] = ws[n][g]. 32 x 32 blocks through LDS (a padded row
+// keeps the column reads conflict free), so both the reads and the writes are 128-byte runs.
+// 256 threads: thread (tx, ty) moves rows ty, ty + 8, ty + 16, ty + 24 of the block.
+__global__ __launch_bounds__(256) void scales_kn_kernel(const float* __restrict__ ws, float* __restrict__ kn, int N,
+                                                        int groups) {
+  __shared__ float tile[32][33];
+  const int tx = threadIdx.x & 31, ty = threadIdx.x >> 5;
+  const int n0 = blockIdx.x * 32, g0 = blockIdx.y * 32;
+#pragma unroll
+  for (int r = 0; r < 32; r += 8) {
+    const int n = n0 + ty + r, g = g0 + tx;
+    if (n < N && g < groups) tile[ty + r][tx] = ws[(size_t)n * groups + g];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int r = 0; r < 32; r += 8) {
+    const int g = g0 + ty + r, n = n0 + tx;
+    if (n < N && g < groups) kn[(size_t)g * N + n] = tile[tx][ty + r];
+  }
+}
+
 // Per-column L1 norms of the dequantized weight, one wave per column (4 per workgroup), and the
 // workgroup's maximum into partial[blockIdx.x]: sum over groups of |s_g| * sum of |codes| (the
 // integer sums are exact; the fp32 products and sum round, which the 2^-10 margin of the final
@@ -692,7 +720,8 @@ static hipError_t launch_cfg(const W4A16Params& p, hipStream_t stream) {
   if (cut > 0) {
     hipLaunchKernelGGL((w4a16_gemm_kernel<kBf16, WM, true, kKTail>), dim3(cut * p.ksplit), dim3(64 * kWaves), 0,
                        stream, p);
-    hipLaunchKernelGGL(w4a16_reduce_kernel, dim3((BM * BN + 1023) / 1024, cut), dim3(256), 0, stream, p, BM, BN);
+    hipLaunchKernelGGL(w4a16_reduce_kernel, dim3((BM * BN + 1023) / 1024, cut), dim3(256), 0, stream, p, BM, BN,
+                       kGroupM);
   }
   return hipGetLastError();
 }
@@ -744,6 +773,14 @@ hipError_t rows_to_scaled_f16_launch(int dtype, const void* x, void* x16, float*
   }
 }
 
+hipError_t w4a16_reduce_launch(const W4A16Params& p, int BM, int BN, int group_m, hipStream_t stream) {
+  const int cut = p.tiles_m * p.tiles_n - p.dp_tiles;
+  if (cut > 0)
+    hipLaunchKernelGGL(w4a16_reduce_kernel, dim3((BM * BN + 1023) / 1024, cut), dim3(256), 0, stream, p, BM, BN,
+                       group_m);
+  return hipGetLastError();
+}
+
 hipError_t w4a16_out_bound_launch(const void* w_q4, const float* w_scale, const void* bias, int bias_dtype, int64_t N,
                                   int64_t K, float* bound, hipStream_t stream) {
   const int np = (int)((N + 3) / 4);
@@ -751,6 +788,12 @@ hipError_t w4a16_out_bound_launch(const void* w_q4, const float* w_scale, const 
                      (int)N, (int)K, bound + 2);
   hipLaunchKernelGGL(w4a16_bound_reduce_kernel, dim3(1), dim3(256), 0, stream, (const float*)(bound + 2), np, bias,
                      bias_dtype, (int)N, bound);
+  return hipGetLastError();
+}
+
+hipError_t scales_kn_launch(const float* w_scale, float* w_scale_kn, int64_t N, int64_t groups, hipStream_t stream) {
+  hipLaunchKernelGGL(scales_kn_kernel, dim3((unsigned)((N + 31) / 32), (unsigned)((groups + 31) / 32)), dim3(256), 0,
+                     stream, w_scale, w_scale_kn, (int)N, (int)groups);
   return hipGetLastError();
 }
 

@@ -71,10 +71,13 @@ __device__ __forceinline__ int swz_b(int n) { return ((n >> 3) & 1) ^ ((n >> 4) 
 // Waves sit kWavesM (along M) x kWavesN (along N); each owns (32 WM) rows x (32 WN) columns as
 // WM x WN blocks of v_mfma_f32_32x32x16. The tile is BM = 32 WM kWavesM rows by
 // BN = 32 WN kWavesN columns.
-// A workgroup computes sub-tile (g % kSub) along M of the 256 x 256 tile p.tile_base + g / kSub
+// A workgroup computes sub-tile (g % kSub) along M of the (kSub BM) x 256 tile p.tile_base + g / kSub
 // (grouped tile order): kSub = 1 for whole tiles, 2 for the 128-row halves that the last,
-// partly filled round of tiles is cut into.
-template <bool kBf16, int kWavesM, int kWavesN, int WM, int WN, int kSub>
+// partly filled round of 256-row tiles is cut into. kCut: K piece g % ksplit of the BM x 256 tile
+// p.tile_base + g / ksplit, its fp32 partial written to slot g of p.partial (summed, with the
+// epilogue, by w4a16_reduce_kernel) -- for the few-tile shapes of small M, where whole tiles would
+// leave most CUs idle.
+template <bool kBf16, int kWavesM, int kWavesN, int WM, int WN, int kSub, bool kCut = false, int kNBuf = kT256NBuf>
 __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W4A16Params p) {
   constexpr int kWaves = kWavesM * kWavesN;
   constexpr int BM = 32 * WM * kWavesM, BN = 32 * WN * kWavesN;
@@ -88,7 +91,8 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W
   constexpr int nL = nA + nB + nS;
   static_assert(nA * 8 * kWaves == BM && nB * 32 * kWaves == BN && nB >= 1, "DMA blocks must split evenly");
   static_assert(nL <= 4 * WM * WN, "the loads of a stage are spread over the MFMAs of a stage");
-  __shared__ __attribute__((aligned(1024))) uint8_t lds[kT256NBuf * kStageBytes];
+  static_assert(kNBuf >= 3 && kNBuf * kStageBytes <= 160 * 1024, "stage ring: 3 or more buffers in 160 KiB of LDS");
+  __shared__ __attribute__((aligned(1024))) uint8_t lds[kNBuf * kStageBytes];
 
   const int lane = threadIdx.x & 63;
   // the wave index is uniform across the wave: in a scalar register, LDS destinations of the DMA
@@ -99,11 +103,18 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W
   const int M = p.M, N = p.N, K = p.K;
   const int S = K / kT256StageK;
 
-  static_assert(BM * kSub == 256 && BN == 256, "sub-tiles of a 256 x 256 tile");
+  static_assert((BM * kSub == 256 || kSub == 1) && BN == 256 && (!kCut || kSub == 1), "sub-tiles of a 256 x 256 tile");
   const int g = xcd_remap(blockIdx.x, gridDim.x);
   int tm, tn;
-  tile_coords(p.tile_base + g / kSub, p.tiles_m, p.tiles_n, kT256GroupM, tm, tn);
-  const int m0 = tm * 256 + (g % kSub) * BM, n0 = tn * BN;
+  tile_coords(p.tile_base + (kCut ? g / p.ksplit : g / kSub), p.tiles_m, p.tiles_n, kT256GroupM, tm, tn);
+  const int m0 = tm * (BM * kSub) + (kCut ? 0 : (g % kSub) * BM), n0 = tn * BN;
+  // this workgroup's stages [sb, sb + Sl): all of K, or K piece g % ksplit
+  int sb = 0, Sl = S;
+  if constexpr (kCut) {
+    const int piece = g % p.ksplit;
+    sb = (int)((long long)piece * S / p.ksplit);
+    Sl = (int)((long long)(piece + 1) * S / p.ksplit) - sb;
+  }
   // The second 128-row half of the last tile row lies wholly past M when M % 256 is in (0, 128]:
   // nothing to compute or store. The exit is uniform over the workgroup and precedes every barrier
   // and DMA. (Without it `rows` would be negative and the activation descriptor's range would wrap
@@ -113,7 +124,17 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W
 
   const rsrc_t rs_a = make_rsrc((const uint16_t*)p.x + (size_t)m0 * K, (uint32_t)rows * K * 2);
   const rsrc_t rs_b = make_rsrc((const uint8_t*)p.wq + (size_t)n0 * (K / 2), (uint32_t)cols * (K / 2));
-  const rsrc_t rs_s = make_rsrc(p.ws + (size_t)n0 * (K / 32), (uint32_t)cols * (K / 32) * 4);
+  // Group scales, column-major [N, K/32] (the reference's layout): a stage's two groups of a column
+  // are 8 bytes of that column's own row, so every column costs a memory request per stage (256
+  // requests of 8 bytes: measured to halve the weight stream's rate where it is memory-bound).
+  // Group-major [K/32, N] (scales_kn): a stage's scales of the tile are two 1 KiB runs. The range
+  // ends at the tile's last column of the last group row; a column past N in an earlier row reads
+  // a scale of the next row, which only enters that column's own accumulators (each output column
+  // has its own weights and scales), and those are never stored.
+  const int kn = p.scales_kn;
+  const rsrc_t rs_s = kn ? make_rsrc(p.ws + n0, (uint32_t)((K / 32 - 1) * N + cols) * 4)
+                         : make_rsrc(p.ws + (size_t)n0 * (K / 32), (uint32_t)cols * (K / 32) * 4);
+  const uint32_t s_stage = kn ? (uint32_t)N * 8 : 8u;  // bytes from one stage's scales to the next
   const rsrc_t rs_none = make_rsrc(p.ws, 0);
 
   // ---- DMA lane offsets (fixed for the K loop; the stage goes into the scalar offset) --------
@@ -132,25 +153,27 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W
   for (int q = 0; q < nB; ++q) {
     const int n = 32 * (w * nB + q) + (lane >> 1);
     vo_b[q] = (uint32_t)n * (K / 2) + 16 * ((lane & 1) ^ swz_b(n));
-    vo_s[q] = ((uint32_t)n * (K / 32) + (lane & 1)) * 4;
+    vo_s[q] = kn ? ((uint32_t)(lane & 1) * N + n) * 4 : ((uint32_t)n * (K / 32) + (lane & 1)) * 4;
   }
 
   // LDS layout: the three activation stage buffers, then the three weight buffers, then the three
   // scale buffers, so that every operand read of buffers 0 and 1 (and the weight and scale reads of
   // all three) fits the 16-bit immediate offset of ds_read from one base register.
-  constexpr int kOffB = kT256NBuf * kABytes, kOffS = kOffB + kT256NBuf * kBBytes;
+  constexpr int kOffB = kNBuf * kABytes, kOffS = kOffB + kNBuf * kBBytes;
   // DMA instruction l (0 .. nL-1) of this wave's share of stage s into ring buffer `buf`. A stage
   // past the end loads through an empty resource (no traffic, no branch).
+  // (s counts this workgroup's stages; the K position is sb + s)
   auto load_one = [&](int l, int s, int buf) {
-    const bool live = s < S;
+    const bool live = s < Sl;
+    const int sg = sb + s;
     if (l < nA) {
-      buf_load16_lds(live ? rs_a : rs_none, lds + buf * kABytes + (w * nA + l) * 1024, vo_a[l], s * 128);
+      buf_load16_lds(live ? rs_a : rs_none, lds + buf * kABytes + (w * nA + l) * 1024, vo_a[l], sg * 128);
     } else if (l < nA + nB) {
       const int q = l - nA;
-      buf_load16_lds(live ? rs_b : rs_none, lds + kOffB + buf * kBBytes + (w * nB + q) * 1024, vo_b[q], s * 32);
+      buf_load16_lds(live ? rs_b : rs_none, lds + kOffB + buf * kBBytes + (w * nB + q) * 1024, vo_b[q], sg * 32);
     } else {
       const int q = l - nA - nB;
-      buf_load4_lds(live ? rs_s : rs_none, lds + kOffS + buf * kSBytes + (w * nS + q) * 256, vo_s[q], s * 8);
+      buf_load4_lds(live ? rs_s : rs_none, lds + kOffS + buf * kSBytes + (w * nS + q) * 256, vo_s[q], sg * s_stage);
     }
   };
   auto load_stage = [&](int s, int buf) {
@@ -167,7 +190,15 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W
   typedef __attribute__((address_space(3))) const u32x4* lds_frag_ptr;
   const uint32_t lds_base = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) uint8_t*)lds;
   constexpr int kImm = 65536;  // ds_read immediate offsets are below 64 KiB
-  constexpr int kFarBuf = (kT256NBuf - 1) * kABytes + 32 * (WM - 1) * 128 >= kImm ? kT256NBuf - 1 : kT256NBuf;
+  // buffers [0, kFarBuf) are read from a_base, the rest from a_far; each group's immediates (buffer
+  // offset + m-block offset, up to 4 KiB (WM - 1)) stay below 64 KiB
+  constexpr int kFarBuf = [] {
+    int f = kNBuf;
+    while (f > 1 && (f - 1) * kABytes + 4096 * (WM - 1) >= kImm) --f;
+    return f;
+  }();
+  static_assert(kFarBuf == kNBuf || (kNBuf - 1 - kFarBuf) * kABytes + 4096 * (WM - 1) < kImm,
+                "activation buffers must split into two groups within the ds_read immediate range");
   uint32_t a_base[4], a_far[4];
 #pragma unroll
   for (int t = 0; t < 4; ++t) {
@@ -208,22 +239,23 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W
   }
 
   // ---- main loop ----------------------------------------------------------------------------
-  // Stage s sits in ring buffer s % 3. Entering stage s: its raw weights, scales and the
-  // activation fragments of K-step 0 are in registers (reads issued), the loads of stage s+1
-  // are in flight, and buffer (s+2) % 3 = (s-1) % 3 is free (every wave passed the barrier at the
-  // end of stage s-1). During stage s each wave issues its loads of stage s+2 into that buffer,
+  // Stage s sits in ring buffer s % kNBuf. Entering stage s: its raw weights, scales and the
+  // activation fragments of K-step 0 are in registers (reads issued), the loads of stages s+1 ..
+  // s+kNBuf-2 are in flight, and buffer (s-1) % kNBuf is free (every wave passed the barrier at
+  // the end of stage s-1). During stage s each wave issues its loads of stage s+kNBuf-1 into it,
   // spread evenly over the stage's MFMAs: issued in a burst, the DMA instructions of all waves
   // fill the texture unit's address FIFO and stall the MFMAs queued behind them. Before the
   // stage's last K-step every wave waits for its own loads of s+1 and passes the barrier (after
-  // which stage s+1 is complete in LDS and nobody reads buffer s % 3 any more); the last
+  // which stage s+1 is complete in LDS and nobody reads buffer s % kNBuf any more); the last
   // K-step's MFMAs then cover the reads of s+1's first fragments.
   // Each activation fragment register is refilled in place with the fragment of the next K-step
   // (of the next stage after the last K-step) right after its last MFMA of this K-step, so the
   // reads have the rest of the K-step's MFMAs to land and only one set of fragments is live.
   constexpr int kSlots = 4 * WM * WN;  // MFMAs per wave and stage
-  // DMA instruction l of stage s+2 goes after MFMA slot l * kSlots / nL of stage s; the ones before
-  // the last K-step (slot < 3 WM WN) are issued before that K-step's wait, which must let exactly
-  // those stay outstanding (vmcnt counts this wave's loads in issue order)
+  // DMA instruction l of stage s+kNBuf-1 goes after MFMA slot l * kSlots / nL of stage s; the ones
+  // before the last K-step (slot < 3 WM WN) are issued before that K-step's wait, which must let
+  // exactly those and the loads of stages s+2 .. s+kNBuf-2 stay outstanding (vmcnt counts this
+  // wave's loads in issue order)
   constexpr int kPreWait = [] {
     int c = 0;
     for (int l = 0; l < nL; ++l) c += (l * kSlots / nL < 3 * WM * WN) ? 1 : 0;
@@ -244,7 +276,7 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W
   };
   auto stage = [&](auto bc, int s) {
     constexpr int bf = decltype(bc)::value;
-    constexpr int bf1 = (bf + 1) % kT256NBuf, bf2 = (bf + 2) % kT256NBuf;
+    constexpr int bf1 = (bf + 1) % kNBuf, bfl = (bf + kNBuf - 1) % kNBuf;
     float n8s[WN];
 #pragma unroll
     for (int i = 0; i < WN; ++i) {
@@ -259,7 +291,7 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W
         // this wave's reads of buffer bf are complete (the last ones fill a[] for this K-step)
         // and its loads of stage s+1 have landed; after the barrier every wave's have
         wait_lgkm();
-        wait_vmcnt<kPreWait>();
+        wait_vmcnt<(kNBuf - 3) * nL + kPreWait>();
         barrier_no_fence();
         first_weights(ic<bf1>{});
       }
@@ -272,7 +304,7 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W
           static_for<0, nL>([&](auto lc) {
             constexpr int l = decltype(lc)::value;
             if constexpr (l * kSlots / nL == slot) {
-              load_one(l, s + 2, bf2);
+              load_one(l, s + kNBuf - 1, bfl);
               __builtin_amdgcn_sched_barrier(0);
             }
           });
@@ -284,7 +316,7 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W
     });
   };
 
-  // ---- prologue: stages 0 and 1 in flight, stage 0 published --------------------------------
+  // ---- prologue: stages 0 .. kNBuf-2 in flight, stage 0 published ---------------------------
   // The column factors load first; csd is formed after the wait for stage 0, so their latency
   // hides behind the stage loads.
   {
@@ -296,9 +328,9 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W
       csd[i] = (cs_p && n < N) ? cs_p[n] : 1.0f;
     }
   }
-  load_stage(0, 0);
-  load_stage(1, 1);
-  wait_vmcnt<nL>();
+#pragma unroll
+  for (int i = 0; i < kNBuf - 1; ++i) load_stage(i, i);
+  wait_vmcnt<(kNBuf - 2) * nL>();
 #pragma unroll
   for (int i = 0; i < WN; ++i) csd[i] = pow2_recip(csd[i]);
   barrier_no_fence();
@@ -307,13 +339,41 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W
   for (int j = 0; j < WM; ++j) a[j] = read_a(0, 0, j);
 
   int s = 0;
-  for (; s + 3 <= S; s += 3) {
-    stage(ic<0>{}, s);
-    stage(ic<1>{}, s + 1);
-    stage(ic<2>{}, s + 2);
+  if constexpr (kNBuf == 3) {
+    // (written out: the generic form below costs the register-tight 256 x 64-per-wave variant
+    // a spill of its accumulators)
+    for (; s + 3 <= Sl; s += 3) {
+      stage(ic<0>{}, s);
+      stage(ic<1>{}, s + 1);
+      stage(ic<2>{}, s + 2);
+    }
+    if (s < Sl) stage(ic<0>{}, s++);
+    if (s < Sl) stage(ic<1>{}, s++);
+  } else {
+    for (; s + kNBuf <= Sl; s += kNBuf) static_for<0, kNBuf>([&](auto bc) { stage(bc, s + decltype(bc)::value); });
+    // the last Sl % kNBuf stages (s is a multiple of kNBuf here: stage s + b sits in buffer b)
+    static_for<0, kNBuf - 1>([&](auto bc) {
+      if (s + decltype(bc)::value < Sl) stage(bc, s + decltype(bc)::value);
+    });
   }
-  if (s < S) stage(ic<0>{}, s++);
-  if (s < S) stage(ic<1>{}, s++);
+
+  if constexpr (kCut) {
+    wait_vmcnt<0>();  // the DMA issued for stages past the piece (zeros into LDS) has landed
+    // K piece: the raw fp32 accumulators to partial slot g, a [BM][BN] row-major tile; lane (c32, h)
+    // of block (i, j) holds row 32j + c32 (of this wave's rows), columns 8 bq + 4h .. +3 of n-block i
+    float* dst = p.partial + (size_t)g * (BM * BN);
+#pragma unroll
+    for (int j = 0; j < WM; ++j)
+#pragma unroll
+      for (int i = 0; i < WN; ++i)
+#pragma unroll
+        for (int bq = 0; bq < 4; ++bq) {
+          const int r = wm * 32 * WM + 32 * j + c32, c = wn * 32 * WN + 32 * i + 8 * bq + 4 * h;
+          *(f32x4*)(dst + (size_t)r * BN + c) =
+              f32x4{acc[i][j][4 * bq], acc[i][j][4 * bq + 1], acc[i][j][4 * bq + 2], acc[i][j][4 * bq + 3]};
+        }
+    return;
+  }
 
   // ---- epilogue ----------------------------------------------------------------------------
   // v = acc * row_scale * col_scale + bias (both scales exact powers of two); with the GELU
@@ -426,7 +486,7 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W
       // last MFMA and the DMA loads issued for stages past the end (which write zeros) have landed.
       constexpr int kHalfRows = BM / 2;
       constexpr int kChunks = BN / 8;  // 16-byte chunks per row
-      static_assert(kHalfRows * BN * 2 <= kT256NBuf * kStageBytes, "half a tile must fit the stage buffers");
+      static_assert(kHalfRows * BN * 2 <= kNBuf * kStageBytes, "half a tile must fit the stage buffers");
       wait_vmcnt<0>();
       wait_lgkm();
       barrier_no_fence();
@@ -517,13 +577,49 @@ hipError_t launch_variant(const W4A16Params& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// Stage buffers of the short tiles: as many as fit 160 KiB of LDS (64 rows: 8 x 18 KiB, 128 rows:
+// 6 x 26 KiB). With few rows a stage is a few hundred cycles of MFMA, far less than a trip to
+// HBM, so only a deep ring of loads in flight keeps the weight stream going.
+constexpr int rows_nbuf(int wm) { return wm == 2 ? 8 : wm == 4 ? 6 : kT256NBuf; }
+
+// Variant 1 with tiles of p.tile_rows (64, 128 or 256) rows: the first dp_tiles whole, the rest cut
+// into ksplit K pieces whose partials w4a16_reduce_kernel sums (tile order of this kernel).
+template <bool kBf16, int WM>
+hipError_t launch_rows(const W4A16Params& p, hipStream_t stream) {
+  constexpr int kNB = rows_nbuf(WM);
+  W4A16Params q = p;
+  const int tiles = p.tiles_m * p.tiles_n;
+  if (p.dp_tiles > 0) {
+    q.tile_base = 0;
+    hipLaunchKernelGGL((w4a16_tile256_kernel<kBf16, 1, 8, WM, 1, 1, false, kNB>), dim3(p.dp_tiles), dim3(512), 0,
+                       stream, q);
+  }
+  const int cut = tiles - p.dp_tiles;
+  if (cut > 0) {
+    q.tile_base = p.dp_tiles;
+    hipLaunchKernelGGL((w4a16_tile256_kernel<kBf16, 1, 8, WM, 1, 1, true, kNB>), dim3(cut * p.ksplit), dim3(512), 0,
+                       stream, q);
+    const hipError_t e = w4a16_reduce_launch(q, 32 * WM, 256, kTile256GroupM, stream);
+    if (e != hipSuccess) return e;
+  }
+  return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t w4a16_tile256_launch(int variant, bool bf16, const W4A16Params& p, hipStream_t stream) {
   switch (variant) {
     case 0:  // 8 waves, 2 x 4, each 128 x 64
       return bf16 ? launch_variant<true, 2, 4, 4, 2>(p, stream) : launch_variant<false, 2, 4, 4, 2>(p, stream);
-    case 1:  // 8 waves, 1 x 8, each 256 x 32
+    case 1:  // 8 waves, 1 x 8, each 256 x 32; with K pieces, or 64 / 128-row tiles, per the plan
+      if (p.ksplit > 1 || p.tile_rows != 256) {
+        switch (p.tile_rows) {
+          case 64: return bf16 ? launch_rows<true, 2>(p, stream) : launch_rows<false, 2>(p, stream);
+          case 128: return bf16 ? launch_rows<true, 4>(p, stream) : launch_rows<false, 4>(p, stream);
+          case 256: return bf16 ? launch_rows<true, 8>(p, stream) : launch_rows<false, 8>(p, stream);
+          default: return hipErrorInvalidValue;
+        }
+      }
       return bf16 ? launch_variant<true, 1, 8, 8, 1>(p, stream) : launch_variant<false, 1, 8, 8, 1>(p, stream);
     case 2:  // 4 waves, 1 x 4, each 256 x 64
       return bf16 ? launch_variant<true, 1, 4, 8, 2>(p, stream) : launch_variant<false, 1, 4, 8, 2>(p, stream);

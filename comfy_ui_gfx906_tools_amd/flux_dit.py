@@ -93,6 +93,28 @@ class Staged(NamedTuple):
     dtype: torch.dtype
 
 
+def _scales_kn(layer, ws: torch.Tensor, rows: slice | None):
+    """The group-major copy of ws (or of its rows `rows`), computed once and kept: on ws for the
+    whole weight, on the layer per row slice (a column slice of the whole copy would not be
+    contiguous). Recomputed after an in-place change of ws or on another stream; None off the GPU
+    or for tensors without a version counter."""
+    if not ws.is_cuda:
+        return None
+    if rows is None:
+        return _lib.cached_scales_kn(ws)
+    try:
+        key = (rows.start, rows.stop, ws._version, torch.cuda.current_stream(ws.device).cuda_stream)
+    except RuntimeError:
+        return None
+    cache = layer.__dict__.setdefault("_qlinear_scales_kn_rows", {})
+    hit = cache.get(key[:2])
+    if hit is not None and hit[0] == key:
+        return hit[1]
+    kn = _lib.w4a16_scales_kn(ws[rows])
+    cache[key[:2]] = (key, kn)
+    return kn
+
+
 def _linear(layer, x, gelu: bool = False, rows: slice | None = None, staged_out: bool = False):
     """layer(x), optionally followed by GELU-tanh, optionally restricted to output rows `rows`
     of the weight. Engine layers fuse the GELU into the GEMM epilogue, take row slices of
@@ -102,8 +124,10 @@ def _linear(layer, x, gelu: bool = False, rows: slice | None = None, staged_out:
     engine layer without rotation or row slice, a Staged bf16 input; otherwise a plain tensor."""
     if _is_engine_linear(layer):
         wq, ws, b = layer.weight_q4, layer.weight_scale, layer.bias
-        # the fp16 dequant's per-column factors, kept with the whole weight (rows slice them)
+        # the fp16 dequant's per-column factors, kept with the whole weight (rows slice them), and
+        # the group-major scale copy of the rows used
         cs = _lib.cached_col_scales(ws) if ws.is_cuda else None
+        kn = _scales_kn(layer, ws, rows)
         if rows is not None:
             wq, ws = wq[rows], ws[rows]
             b = b[rows] if b is not None else None
@@ -114,11 +138,11 @@ def _linear(layer, x, gelu: bool = False, rows: slice | None = None, staged_out:
             bias = b.to(x.dtype) if b is not None else None
             if staged_out and rows is None and x.dtype == torch.bfloat16:
                 y16, rs = _lib.w4a16_gemm(x.x16, wq, ws, bias, out_dtype=x.dtype, row_scale=x.row_scale, gelu=gelu,
-                                          col_scale=cs, f16_rowscaled=True,
+                                          col_scale=cs, scales_kn=kn, f16_rowscaled=True,
                                           out_bound=_lib.cached_out_bound(wq, ws, bias))
                 return Staged(y16, rs, x.lead, x.dtype)
             y = _lib.w4a16_gemm(x.x16, wq, ws, bias, out_dtype=x.dtype, row_scale=x.row_scale, gelu=gelu,
-                                col_scale=cs)
+                                col_scale=cs, scales_kn=kn)
             return y.reshape(*x.lead, wq.shape[0])
         shape = x.shape
         x2 = x.reshape(-1, shape[-1])
@@ -127,10 +151,11 @@ def _linear(layer, x, gelu: bool = False, rows: slice | None = None, staged_out:
             g = layer.rotation_group
             if shape[-1] <= ROTATE_FUSED_MAX_K:
                 x16, rs = _lib.rotate_rows_to_f16(x2, get_group_signs(g, x2.device), g)
-                y = _lib.w4a16_gemm(x16, wq, ws, bias, out_dtype=x.dtype, row_scale=rs, gelu=gelu, col_scale=cs)
+                y = _lib.w4a16_gemm(x16, wq, ws, bias, out_dtype=x.dtype, row_scale=rs, gelu=gelu, col_scale=cs,
+                                    scales_kn=kn)
                 return y.reshape(*shape[:-1], wq.shape[0])
             x2 = apply_group_rotation(x2.float(), get_group_rotation(shape[-1], g, x2.device), g)
-        y = _lib.w4a16_gemm(x2, wq, ws, bias, out_dtype=x.dtype, gelu=gelu, col_scale=cs)
+        y = _lib.w4a16_gemm(x2, wq, ws, bias, out_dtype=x.dtype, gelu=gelu, col_scale=cs, scales_kn=kn)
         return y.reshape(*shape[:-1], wq.shape[0])
     w, b = layer.weight, layer.bias
     if rows is not None:

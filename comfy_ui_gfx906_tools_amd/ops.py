@@ -161,17 +161,20 @@ def int4_linear(x: torch.Tensor, w_packed: torch.Tensor, w_scale: torch.Tensor, 
     shape = x.shape
     K = shape[-1]
     x2d = x.reshape(-1, K)
-    # the fp16 dequant's per-column factors, computed once per weight and kept with it
+    # the fp16 dequant's per-column factors, computed once per weight and kept with it, and the
+    # group-major copy of the scales that the tile kernels (more than 16 rows) read
     cs = _lib.cached_col_scales(w_scale) if w_scale.is_cuda else None
+    kn = _lib.cached_scales_kn(w_scale) if w_scale.is_cuda and x2d.shape[0] > 16 else None
     if rotation_group and x2d.is_cuda and K <= ROTATE_FUSED_MAX_K:
         # rotation and fp16 staging in one pass, then the GEMM on the staged operand
         x16, rs = _lib.rotate_rows_to_f16(x2d, get_group_signs(rotation_group, x2d.device), rotation_group)
-        out = _lib.w4a16_gemm(x16, w_packed, w_scale, bias, out_dtype=x.dtype, row_scale=rs, col_scale=cs)
+        out = _lib.w4a16_gemm(x16, w_packed, w_scale, bias, out_dtype=x.dtype, row_scale=rs, col_scale=cs,
+                              scales_kn=kn)
         return out.reshape(*shape[:-1], w_packed.shape[0])
     if rotation_group:
         R = get_group_rotation(K, rotation_group, x2d.device)
         x2d = apply_group_rotation(x2d.float(), R, rotation_group)
-    out = _lib.w4a16_gemm(x2d, w_packed, w_scale, bias, out_dtype=x.dtype, col_scale=cs)
+    out = _lib.w4a16_gemm(x2d, w_packed, w_scale, bias, out_dtype=x.dtype, col_scale=cs, scales_kn=kn)
     return out.reshape(*shape[:-1], w_packed.shape[0])
 
 

@@ -45,7 +45,8 @@ enum qlinear_status {
 /* Message for the last failing call on this host thread ("" if none). */
 const char* qlinear_last_error(void);
 
-/* ABI version of this header: (major << 16) | minor. 2.0: qlinear_w4a16_gemm takes col_scale. */
+/* ABI version of this header: (major << 16) | minor. 2.0: qlinear_w4a16_gemm takes col_scale;
+ * 3.0: qlinear_w4a16_gemm(_noalloc) take w_scale_kn. */
 int qlinear_abi_version(void);
 
 /* ---------------------------------------------------------------------------------------
@@ -67,6 +68,7 @@ int qlinear_abi_version(void);
  *   K % 32 == 0, K >= 32; M >= 0 (M == 0 launches nothing)
  *   splits    0 = automatic (under-filled last waves are cut into K pieces),
  *             1 = one workgroup per output tile, 2..64 = that many K pieces per tile.
+ *   w_scale_kn [K/32, N] fp32 from qlinear_w4a16_scales_kn(w_scale), or NULL (below).
  *   col_scale [N] fp32 from qlinear_w4a16_col_scales(w_scale), or NULL (then computed into the
  *             workspace by the call); read only by the tile kernels on the fp16 route.
  *   workspace device memory of qlinear_w4a16_workspace_bytes(...) bytes (NULL when that is 0),
@@ -109,10 +111,23 @@ size_t qlinear_w4a16_workspace_bytes(int x_dtype, int64_t M, int64_t N, int64_t 
                                      int flags, int device);
 
 int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const float* row_scale,
-                       const void* w_q4, const float* w_scale, const float* col_scale,
-                       const void* bias, void* y, const float* out_bound, float* out_row_scale,
-                       int64_t M, int64_t N, int64_t K, int splits, int flags, void* workspace,
-                       size_t workspace_bytes, void* stream);
+                       const void* w_q4, const float* w_scale, const float* w_scale_kn,
+                       const float* col_scale, const void* bias, void* y, const float* out_bound,
+                       float* out_row_scale, int64_t M, int64_t N, int64_t K, int splits, int flags,
+                       void* workspace, size_t workspace_bytes, void* stream);
+
+/* Group-major copy of the group scales: w_scale_kn[g * N + n] = w_scale[n * (K/32) + g]
+ * ([K/32, N] fp32, N * K / 8 bytes). Passed as w_scale_kn to qlinear_w4a16_gemm (NULL there =
+ * read w_scale), the tile kernels (configurations 0-6) read it instead of w_scale: a stage of a
+ * 256-column tile then needs its scales as a few runs of 1 KiB rather than 8-16 bytes from each of
+ * 256 column rows. Measured on MI355X for a weight stream like the skinny-M GEMMs' (N = 65536,
+ * K = 4096, no arithmetic): 68 us with the column rows, 40 us group-major, 35 us with no scales
+ * at all. The results are the same bit for bit; only the addresses change. w_scale itself is
+ * still read by the direct kernels (7, 8: whole column rows, already long runs) and by the
+ * column-factor pass. Depends only on w_scale: compute once per weight and keep it with the
+ * weight. No counterpart in the reference (its scales stay [N, K/32]). */
+int qlinear_w4a16_scales_kn(const float* w_scale, float* w_scale_kn, int64_t N, int64_t K,
+                            void* stream);
 
 /* The weight's output bound for QL_W4A16_F16_ROWSCALED: bound[0] = max_n sum_k |dequant W_nk| *
  * (1 + 2^-10), bound[1] = max_n |bias_n| (0 when bias is NULL). bound holds
@@ -134,10 +149,10 @@ int qlinear_w4a16_out_bound(const void* w_q4, const float* w_scale, const void* 
  * no initial contents (each call writes what it reads). */
 #define QL_W4A16_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
 int qlinear_w4a16_gemm_noalloc(int x_dtype, int out_dtype, const void* x, const float* row_scale,
-                               const void* w_q4, const float* w_scale, const float* col_scale,
-                               const void* bias, void* y, const float* out_bound,
-                               float* out_row_scale, int64_t M, int64_t N, int64_t K, int splits,
-                               int flags, void* stream);
+                               const void* w_q4, const float* w_scale, const float* w_scale_kn,
+                               const float* col_scale, const void* bias, void* y,
+                               const float* out_bound, float* out_row_scale, int64_t M, int64_t N,
+                               int64_t K, int splits, int flags, void* stream);
 
 /* Column factors of the fp16 dequant: col_scale[n] = 2^e_n with 8 * max_g |w_scale[n, g]| * 2^-e_n
  * in [2^14, 2^15) (e_n clamped to [-126, 126]; 1 for a column whose scales are all 0 or not

@@ -39,7 +39,7 @@ def lib():
 def test_header_parses():
     fns = _header_functions()
     assert {"qlinear_w4a16_gemm", "qlinear_w8a8_gemm", "qlinear_quantize_int4", "qlinear_last_error"} <= set(fns)
-    assert fns["qlinear_w4a16_gemm"] == 19 and fns["qlinear_abi_version"] == 0
+    assert fns["qlinear_w4a16_gemm"] == 20 and fns["qlinear_abi_version"] == 0
 
 
 def test_every_declared_symbol_is_exported(lib):
@@ -61,7 +61,7 @@ def test_ctypes_table_matches_header(lib):
 
 
 def test_abi_version_and_error_text(lib):
-    assert lib.qlinear_abi_version() >> 16 == 2
+    assert lib.qlinear_abi_version() >> 16 == 3
     assert isinstance(lib.qlinear_last_error(), bytes)
 
 
@@ -70,7 +70,8 @@ def _err(lib):
 
 
 def test_w4a16_argument_checks(lib):
-    f = lib.qlinear_w4a16_gemm
+    def f(*a):  # every argument but w_scale_kn (NULL: the checks below do not depend on it)
+        return lib.qlinear_w4a16_gemm(*a[:6], None, *a[6:])
     # bad activation dtype (int32)
     assert f(3, 0, None, None, None, None, None, None, None, None, None, 4, 64, 64, 0, 0, None, 0, None) == QL_ERR_DTYPE
     assert "x dtype" in _err(lib)
@@ -112,8 +113,10 @@ def test_w4a16_argument_checks(lib):
     for c in (4, 5, 6):
         assert f(2, 2, None, None, None, None, None, None, None, None, None, 0, 64, 96, 0, cfg(c), None, 0, None) == QL_ERR_SHAPE
         assert "K % 64 == 0" in _err(lib)
+    for c in (4, 6):  # variants 0 and 2 run whole tiles; variant 1 (configuration 5) takes K pieces
         assert f(2, 2, None, None, None, None, None, None, None, None, None, 0, 64, 128, 2, cfg(c), None, 0, None) == QL_ERR_ARG
         assert "whole tiles" in _err(lib)
+    assert f(2, 2, None, None, None, None, None, None, None, None, None, 0, 64, 128, 2, cfg(5), None, 0, None) == QL_OK
 
 
 def test_quantizer_and_w8a8_argument_checks(lib):

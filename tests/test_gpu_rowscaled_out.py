@@ -45,7 +45,8 @@ def test_out_bound_matches_float64():
 
 @pytest.mark.parametrize("M,N,K,cfg,splits", [(300, 1040, 1024, None, 0), (300, 1040, 1024, 5, 0),
                                               (513, 777, 640, 5, 0), (257, 520, 512, 1, 3), (200, 700, 512, 2, 0),
-                                              (40, 600, 512, 3, 0), (600, 256, 3072, None, 0)])
+                                              (40, 600, 512, 3, 0), (600, 256, 3072, None, 0),
+                                              (64, 1040, 1024, 5, 0), (100, 777, 640, 5, 1), (128, 520, 2048, 5, 3)])
 @pytest.mark.parametrize("gelu", [False, True])
 def test_rowscaled_output_equals_bf16_output(M, N, K, cfg, splits, gelu):
     L = _lib()

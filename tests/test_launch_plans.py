@@ -42,7 +42,7 @@ def test_w4a16_plans_every_configuration(lib, cus):
             for xdt in (1, 2):  # fp16 / bf16 x
                 _check(lib, 0, xdt, M, N, K, 0, 0, cus)              # automatic choice
                 for c in range(7):
-                    for splits in ((0, 1) if c >= 4 else (0, 1, 2, 7)):
+                    for splits in ((0, 1) if c in (4, 6) else (0, 1, 2, 7)):
                         _check(lib, 0, xdt, M, N, K, splits, flags_cfg(c), cus)
 
 
@@ -80,3 +80,28 @@ def test_describe_plan():
     assert _lib.w4a16_describe_plan(1, 10240, 4096, cus=256)["config"] == 7
     assert _lib.w4a16_describe_plan(16, 10240, 4096, cus=256)["config"] == 8
     assert _lib.w4a16_describe_plan(64, 10240, 4096, cus=256)["config"] == 2
+    assert _lib.w4a16_describe_plan(100, 10240, 4032, cus=256)["config"] == 1
+    assert _lib.w4a16_describe_plan(256, 10240, 4096, cus=256)["config"] == 1
+
+
+def test_describe_plan_row_tiles():
+    """Configuration 5 forced at small M: the shortest tile height that covers M (64 / 128 / 256),
+    and K pieces enough for one per CU when the tiles fill fewer than half of them (each piece at
+    least 4 stages of 64); an explicit split count is taken as given (up to the stage count)."""
+    from comfy_ui_gfx906_tools_amd import _lib
+    if not os.path.exists(LIB):
+        pytest.skip("libqlinear.so not built")
+    d = _lib.w4a16_describe_plan(64, 10240, 4096, config=5, cus=256)
+    assert (d["tile_rows"], d["tiles"], d["whole_tiles"], d["k_pieces"]) == (64, 40, 0, 6)
+    d = _lib.w4a16_describe_plan(100, 10240, 4096, config=5, cus=256)
+    assert (d["tile_rows"], d["k_pieces"]) == (128, 6)
+    d = _lib.w4a16_describe_plan(256, 10240, 4096, config=5, cus=256)
+    assert (d["tile_rows"], d["k_pieces"]) == (256, 6)
+    d = _lib.w4a16_describe_plan(64, 10240, 512, config=5, cus=256)  # 8 stages: 2 pieces of 4
+    assert d["k_pieces"] == 2
+    d = _lib.w4a16_describe_plan(64, 40960, 4096, config=5, cus=256)  # 160 tiles: whole
+    assert (d["tile_rows"], d["whole_tiles"], d["k_pieces"]) == (64, 160, 1)
+    d = _lib.w4a16_describe_plan(64, 10240, 4096, config=5, splits=3, cus=256)
+    assert (d["whole_tiles"], d["k_pieces"]) == (0, 3)
+    d = _lib.w4a16_describe_plan(64, 10240, 4096, config=5, splits=1, cus=256)
+    assert (d["whole_tiles"], d["k_pieces"]) == (40, 1)
