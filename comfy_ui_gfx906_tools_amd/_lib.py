@@ -26,6 +26,7 @@ _DTYPE_CODE = {torch.float32: QL_F32, torch.float16: QL_F16, torch.bfloat16: QL_
 W4A16_BF16_MFMA = 1  # flags: bf16 activations straight into bf16 MFMA (see include/qlinear.h)
 W4A16_GELU_TANH = 2  # flags: fused GELU-tanh epilogue
 W4A16_F16_ROWSCALED = 4  # flags: output stored as the next GEMM's row-scaled fp16 operand
+W4A16_GATED_RESIDUAL = 16  # flags: y = residual + gate * output (ql_w4a16_residual)
 W4A16_CFG_SHIFT = 8  # flags bits 8-11: forced kernel configuration + 1 (QL_W4A16_CFG)
 W4A16_TILE256 = 4    # configuration id of the 256 x 256, 8-wave kernel
 W4A16_NOALLOC_SCRATCH_BYTES = 32 << 20  # QL_W4A16_NOALLOC_SCRATCH_BYTES
@@ -47,12 +48,12 @@ SIGNATURES = {
     "qlinear_abi_version": (_c_int, []),
     "qlinear_w4a16_workspace_bytes": (_c_size_t, [_c_int, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_int]),
     "qlinear_w4a16_gemm": (_c_int, [_c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
-                                    _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_vp, _c_size_t, _c_vp]),
+                                    _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_vp, _c_size_t, _c_vp]),
     "qlinear_w4a16_scales_kn": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
     "qlinear_w4a16_col_scales": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
     "qlinear_w4a16_out_bound": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_i64, _c_i64, _c_vp, _c_vp]),
     "qlinear_w4a16_gemm_noalloc": (_c_int, [_c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
-                                            _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_vp]),
+                                            _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_vp]),
     "qlinear_rows_to_f16": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
     "qlinear_w4a16_auto_splits": (_c_int, [_c_i64, _c_i64, _c_i64, _c_int]),
     "qlinear_quantize_int4": (_c_int, [_c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
@@ -77,6 +78,11 @@ SIGNATURES = {
                                            _c_vp]),
     "qlinear_gated_residual": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
 }
+
+
+class Residual(ctypes.Structure):
+    """ql_w4a16_residual of include/qlinear.h."""
+    _fields_ = [("residual", ctypes.c_void_p), ("gate", ctypes.c_void_p), ("gate_rows", ctypes.c_int64)]
 
 
 def load_library(path: str = LIB_PATH):
@@ -283,7 +289,8 @@ def w4a16_gemm(x: torch.Tensor, w_q4: torch.Tensor, w_scale: torch.Tensor, bias:
                row_scale: torch.Tensor | None = None, config: int | None = None,
                gelu: bool = False, col_scale: torch.Tensor | None = None, noalloc: bool = False,
                f16_rowscaled: bool = False, out_bound: torch.Tensor | None = None,
-               scales_kn: torch.Tensor | None = None):
+               scales_kn: torch.Tensor | None = None, residual: torch.Tensor | None = None,
+               gate: torch.Tensor | None = None, out: torch.Tensor | None = None):
     """y[M, N] = x[M, K] @ dequant(w_q4, w_scale)^T (+ bias) on the gfx950 W4A16 kernel.
     x: fp16/bf16/fp32 [M, K]; w_q4: int8 [N, K/2]; w_scale: fp32 [N, K/32]; bias: out_dtype [N].
     bf16 and fp32 activations go through the exact row-scaled fp16 staging unless bf16_mfma is
@@ -298,7 +305,11 @@ def w4a16_gemm(x: torch.Tensor, w_q4: torch.Tensor, w_scale: torch.Tensor, bias:
     f16_rowscaled: the bf16 result (out_dtype must be bfloat16) stored as the next GEMM's row-scaled
     fp16 operand (QL_W4A16_F16_ROWSCALED); returns (y16 fp16 [M, N], row_scale fp32 [M]) to pass on
     as (x, row_scale). out_bound: w4a16_out_bound of this weight and bias (computed when None).
-    scales_kn: w4a16_scales_kn of this w_scale (group-major, read by the tile kernels), or None."""
+    scales_kn: w4a16_scales_kn of this w_scale (group-major, read by the tile kernels), or None.
+    residual, gate: the gated residual epilogue (QL_W4A16_GATED_RESIDUAL), y = residual + gate * y:
+    residual out_dtype [M, N]; gate out_dtype [G, N] with M % G == 0, row m taking gate row
+    m // (M // G) (G = the batch of a [B, L, N] activation). out: the output tensor (out_dtype
+    [M, N], contiguous), e.g. residual itself for the in-place update; None = a new tensor."""
     lib = load_library()
     x = _dev_tensor(x, "x")
     w_q4 = _dev_tensor(w_q4, "w_q4")
@@ -323,7 +334,29 @@ def w4a16_gemm(x: torch.Tensor, w_q4: torch.Tensor, w_scale: torch.Tensor, bias:
         bias = _dev_tensor(bias, "bias")
         if bias.dtype != out_dtype or bias.numel() != N:
             raise RuntimeError(f"bias must be {out_dtype} [{N}], got {bias.dtype} {tuple(bias.shape)}")
-    y = torch.empty((M, N), dtype=torch.float16 if f16_rowscaled else out_dtype, device=x.device)
+    if out is not None:
+        if f16_rowscaled or out.dtype != out_dtype or tuple(out.shape) != (M, N) or not out.is_contiguous() \
+                or out.device != x.device:
+            raise RuntimeError(f"out must be a contiguous {out_dtype} [{M}, {N}] tensor on {x.device}")
+        y = out
+    else:
+        y = torch.empty((M, N), dtype=torch.float16 if f16_rowscaled else out_dtype, device=x.device)
+    res_arg = None
+    if residual is not None or gate is not None:
+        if residual is None or gate is None:
+            raise RuntimeError("the gated residual needs both residual and gate")
+        residual, gate = _dev_tensor(residual, "residual"), _dev_tensor(gate, "gate")
+        if residual.dtype != out_dtype or tuple(residual.shape) != (M, N) or not residual.is_contiguous():
+            raise RuntimeError(f"residual must be a contiguous {out_dtype} [{M}, {N}] tensor, got {residual.dtype} "
+                               f"{tuple(residual.shape)}")
+        gate2 = gate.reshape(-1, N).contiguous() if N and gate.numel() % N == 0 else gate
+        G = gate2.shape[0] if gate2.dim() == 2 else 0
+        if gate.dtype != out_dtype or G < 1 or M % G != 0:
+            raise RuntimeError(f"gate must be a {out_dtype} [G, {N}] tensor with {M} % G == 0, got "
+                               f"{gate.dtype} {tuple(gate.shape)}")
+        if residual.device != x.device or gate.device != x.device:
+            raise RuntimeError("residual and gate must be on the device of x")
+        res_arg = Residual(residual.data_ptr(), gate2.data_ptr(), M // G if M else 1)
     out_rs = None
     if f16_rowscaled:
         if out_dtype != torch.bfloat16:
@@ -335,7 +368,8 @@ def w4a16_gemm(x: torch.Tensor, w_q4: torch.Tensor, w_scale: torch.Tensor, bias:
     if M == 0:
         return (y, out_rs) if f16_rowscaled else y
     flags = (W4A16_BF16_MFMA if bf16_mfma else 0) | (W4A16_GELU_TANH if gelu else 0) | \
-        (W4A16_F16_ROWSCALED if f16_rowscaled else 0)
+        (W4A16_F16_ROWSCALED if f16_rowscaled else 0) | (W4A16_GATED_RESIDUAL if res_arg is not None else 0)
+    res_ptr = ctypes.addressof(res_arg) if res_arg is not None else None
     if config is not None:
         flags |= (int(config) + 1) << W4A16_CFG_SHIFT
     xdt = _DTYPE_CODE[x.dtype]
@@ -364,8 +398,8 @@ def w4a16_gemm(x: torch.Tensor, w_q4: torch.Tensor, w_scale: torch.Tensor, bias:
                                                 col_scale.data_ptr() if col_scale is not None else None,
                                                 bias.data_ptr() if bias is not None else None, y.data_ptr(),
                                                 out_bound.data_ptr() if out_bound is not None else None,
-                                                out_rs.data_ptr() if out_rs is not None else None, M, N, K,
-                                                splits, flags, stream)
+                                                out_rs.data_ptr() if out_rs is not None else None, res_ptr,
+                                                M, N, K, splits, flags, stream)
             _check(rc, "w4a16_gemm_noalloc")
             return (y, out_rs) if f16_rowscaled else y
         nbytes = lib.qlinear_w4a16_workspace_bytes(xdt, M, N, K, splits, flags, x.device.index)
@@ -376,8 +410,8 @@ def w4a16_gemm(x: torch.Tensor, w_q4: torch.Tensor, w_scale: torch.Tensor, bias:
                                     col_scale.data_ptr() if col_scale is not None else None,
                                     bias.data_ptr() if bias is not None else None, y.data_ptr(),
                                     out_bound.data_ptr() if out_bound is not None else None,
-                                    out_rs.data_ptr() if out_rs is not None else None, M, N, K, splits,
-                                    flags, ws.data_ptr() if ws is not None else None,
+                                    out_rs.data_ptr() if out_rs is not None else None, res_ptr, M, N, K,
+                                    splits, flags, ws.data_ptr() if ws is not None else None,
                                     ws.numel() if ws is not None else 0, stream)
     _check(rc, "w4a16_gemm")
     return (y, out_rs) if f16_rowscaled else y

@@ -165,7 +165,8 @@ int skinny_blocks(int64_t M, int64_t N, int cus) {
 // compute; 7 and 8 use the exact codes and are skipped then.
 int w4a16_cfg_for(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, int flags, int cus) {
   // the direct kernels (7, 8) neither compute the bf16-rounded weights nor store row-scaled fp16
-  const bool exact_ok = splits < 2 && !(flags & (QL_W4A16_BF16_MFMA | QL_W4A16_F16_ROWSCALED));
+  const bool exact_ok =
+      splits < 2 && !(flags & (QL_W4A16_BF16_MFMA | QL_W4A16_F16_ROWSCALED | QL_W4A16_GATED_RESIDUAL));
   if (exact_ok && M <= 1 && gemv_fits(x_dtype, M, K)) return kCfgGemv;
   if (exact_ok && skinny_fits(x_dtype, M, N, K)) return kCfgSkinny;
   if (exact_ok && gemv_fits(x_dtype, M, K)) return kCfgGemv;
@@ -279,8 +280,17 @@ int check_w4a16_args(int x_dtype, int out_dtype, const float* row_scale, int64_t
                 out_dtype);
   if (int rc = check_w4a16_shape(M, N, K)) return rc;
   if (splits < 0 || splits > 64) return fail(QL_ERR_ARG, "splits must be in [0, 64], got %d", splits);
-  if (flags & ~(QL_W4A16_BF16_MFMA | QL_W4A16_GELU_TANH | QL_W4A16_F16_ROWSCALED | QL_W4A16_CFG_MASK))
+  if (flags & ~(QL_W4A16_BF16_MFMA | QL_W4A16_GELU_TANH | QL_W4A16_F16_ROWSCALED | QL_W4A16_GATED_RESIDUAL |
+                QL_W4A16_CFG_MASK))
     return fail(QL_ERR_ARG, "unknown flags 0x%x", flags);
+  if (flags & QL_W4A16_GATED_RESIDUAL) {
+    const int forced = (flags & QL_W4A16_CFG_MASK) >> QL_W4A16_CFG_SHIFT;
+    if (flags & QL_W4A16_F16_ROWSCALED)
+      return fail(QL_ERR_ARG, "QL_W4A16_GATED_RESIDUAL and QL_W4A16_F16_ROWSCALED do not combine");
+    if (forced && forced - 1 > kCfgTile256Auto)
+      return fail(QL_ERR_ARG, "QL_W4A16_GATED_RESIDUAL runs on kernel configurations 0-%d, not %d", kCfgTile256Auto,
+                  forced - 1);
+  }
   if (flags & QL_W4A16_F16_ROWSCALED) {
     const int forced = (flags & QL_W4A16_CFG_MASK) >> QL_W4A16_CFG_SHIFT;
     if (out_dtype != QL_BF16)
@@ -377,7 +387,7 @@ extern "C" {
 
 const char* qlinear_last_error(void) { return g_last_error.c_str(); }
 
-int qlinear_abi_version(void) { return (3 << 16) | 0; }
+int qlinear_abi_version(void) { return (4 << 16) | 0; }
 
 size_t qlinear_w4a16_workspace_bytes(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, int flags,
                                      int device) {
@@ -399,12 +409,24 @@ int qlinear_w4a16_auto_splits(int64_t M, int64_t N, int64_t K, int device) {
 
 int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const float* row_scale, const void* w_q4,
                        const float* w_scale, const float* w_scale_kn, const float* col_scale, const void* bias, void* y,
-                       const float* out_bound,
-                       float* out_row_scale, int64_t M, int64_t N, int64_t K, int splits, int flags, void* workspace,
-                       size_t workspace_bytes, void* stream) {
+                       const float* out_bound, float* out_row_scale, const ql_w4a16_residual* residual, int64_t M,
+                       int64_t N, int64_t K, int splits, int flags, void* workspace, size_t workspace_bytes,
+                       void* stream) {
   if (int rc = check_w4a16_args(x_dtype, out_dtype, row_scale, M, N, K, splits, flags)) return rc;
   if ((flags & QL_W4A16_F16_ROWSCALED) && M > 0 && (!out_bound || !out_row_scale))
     return fail(QL_ERR_ARG, "QL_W4A16_F16_ROWSCALED needs out_bound (qlinear_w4a16_out_bound) and out_row_scale [M]");
+  const bool gated = (flags & QL_W4A16_GATED_RESIDUAL) != 0;
+  if (gated != (residual != nullptr))
+    return fail(QL_ERR_ARG, "residual must be given exactly when flags has QL_W4A16_GATED_RESIDUAL");
+  if (gated && M > 0) {
+    const size_t esz = out_dtype == QL_F32 ? 4 : 2;
+    if (!residual->residual || !residual->gate)
+      return fail(QL_ERR_ARG, "null residual / gate pointer in the gated residual");
+    if (residual->gate_rows < 1 || residual->gate_rows > INT32_MAX)
+      return fail(QL_ERR_ARG, "gate_rows must be in [1, 2^31), got %lld", (long long)residual->gate_rows);
+    if (((uintptr_t)residual->residual | (uintptr_t)residual->gate) % esz)
+      return fail(QL_ERR_ALIGN, "residual and gate must be aligned to their %zu-byte elements", esz);
+  }
   if (M == 0) return ok();
   if (!x || !w_q4 || !w_scale || !y) return fail(QL_ERR_ARG, "null x / w_q4 / w_scale / y pointer");
   if (!aligned16(x) || !aligned16(w_q4))
@@ -455,6 +477,11 @@ int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const float* r
   p.out_dtype = (flags & QL_W4A16_F16_ROWSCALED) ? kBF16AsF16 : out_dtype;
   p.out_bound = out_bound;
   p.out_row_scale = out_row_scale;
+  if (gated) {
+    p.residual = residual->residual;
+    p.gate = residual->gate;
+    p.gate_rows = (int)residual->gate_rows;
+  }
   p.act = (flags & QL_W4A16_GELU_TANH) ? kActGeluTanh : kActNone;
   p.cus = cus;
   p.tiles_m = pl.tiles_m;
@@ -475,9 +502,9 @@ int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const float* r
 
 int qlinear_w4a16_gemm_noalloc(int x_dtype, int out_dtype, const void* x, const float* row_scale, const void* w_q4,
                                const float* w_scale, const float* w_scale_kn, const float* col_scale, const void* bias,
-                               void* y,
-                               const float* out_bound, float* out_row_scale, int64_t M, int64_t N, int64_t K,
-                               int splits, int flags, void* stream) {
+                               void* y, const float* out_bound, float* out_row_scale,
+                               const ql_w4a16_residual* residual, int64_t M, int64_t N, int64_t K, int splits,
+                               int flags, void* stream) {
   // the checks qlinear_w4a16_gemm makes before planning, so the size check below sees a valid plan
   if (int rc = check_w4a16_args(x_dtype, out_dtype, row_scale, M, N, K, splits, flags)) return rc;
   if (M == 0) return ok();
@@ -494,7 +521,8 @@ int qlinear_w4a16_gemm_noalloc(int x_dtype, int out_dtype, const void* x, const 
     if (int rc = scratch_address(&ws)) return rc;
   }
   return qlinear_w4a16_gemm(x_dtype, out_dtype, x, row_scale, w_q4, w_scale, w_scale_kn, col_scale, bias, y, out_bound,
-                            out_row_scale, M, N, K, splits, flags, ws, need > 0 ? kNoAllocScratchBytes : 0, stream);
+                            out_row_scale, residual, M, N, K, splits, flags, ws, need > 0 ? kNoAllocScratchBytes : 0,
+                            stream);
 }
 
 int qlinear_w4a16_describe_plan(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, int flags, int cus,

@@ -99,6 +99,34 @@ __device__ __forceinline__ float round_to(int dt, float v) {
   return v;
 }
 
+// Gated residual on 8 consecutive 16-bit outputs (dtype DT, packed pairs in w, each already the
+// rounded output value v): residual + gate * v in fp32 (the product of two 16-bit numbers is
+// exact in fp32, so only the sum rounds before the final rounding to DT). cnt < 8 (the row's end)
+// reads only the first cnt residuals and gates; vec allows the 16-byte loads.
+template <int DT>
+__device__ __forceinline__ u32x4 gated_residual8(u32x4 w, const uint16_t* res, const uint16_t* gate, int cnt,
+                                                 bool vec) {
+  u32x4 r = {0u, 0u, 0u, 0u}, g = {0u, 0u, 0u, 0u};
+  if (vec && cnt == 8) {
+    r = *(const u32x4*)res;
+    g = *(const u32x4*)gate;
+  } else {
+    for (int e = 0; e < cnt; ++e) {
+      r[e >> 1] |= (uint32_t)res[e] << (16 * (e & 1));
+      g[e >> 1] |= (uint32_t)gate[e] << (16 * (e & 1));
+    }
+  }
+  auto f = [](uint32_t bits) { return DT == kBF16 ? bf16_bits_to_f32(bits) : f16_bits_to_f32(bits); };
+  u32x4 o;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const float lo = f(r[q] & 0xFFFFu) + f(g[q] & 0xFFFFu) * f(w[q] & 0xFFFFu);
+    const float hi = f(r[q] >> 16) + f(g[q] >> 16) * f(w[q] >> 16);
+    o[q] = DT == kBF16 ? pack2_bf16(lo, hi) : pack2_f16(lo, hi);
+  }
+  return o;
+}
+
 // GELU, tanh approximation, in fp32: 0.5 x (1 + tanh(u)), u = sqrt(2/pi) (x + 0.044715 x^3), the
 // form of torch.nn.functional.gelu(approximate="tanh") that the reference's DiT MLP applies between
 // its two linears. Evaluated through the identity 0.5 (1 + tanh(u)) =

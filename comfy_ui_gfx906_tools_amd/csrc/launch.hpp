@@ -43,6 +43,13 @@ struct W4A16Params {
   int tile_base;         // 256 x 256 kernel: first tile of the launch (set by the launcher)
   int tile_rows;         // 256-column kernel, variant 1: tile height 64, 128 or 256
   int scales_kn;         // ws is group-major [K/32, N] (qlinear_w4a16_scales_kn)
+  // Gated residual epilogue (or null): y = residual + gate[m / gate_rows] * v, v the output as it
+  // would be stored (rounded to out_dtype), in fp32, rounded once more; residual [M, N] and gate
+  // [ceil(M / gate_rows), N] in out_dtype; y may be residual itself (each element is read and
+  // written by the same thread)
+  const void* residual;
+  const void* gate;
+  int gate_rows;
   int cus;               // compute units of the device (grid sizing)
 };
 

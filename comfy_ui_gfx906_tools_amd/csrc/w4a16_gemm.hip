@@ -334,7 +334,9 @@ __global__ __launch_bounds__(64 * kWaves) void w4a16_gemm_kernel(W4A16Params p) 
   const void* bias = p.bias;
   const float* row_scale = p.row_scale;
   const float* col_scale = p.col_scale;
+  const void* resid = p.residual;
   if constexpr (kCut) {
+    resid = nullptr;
     dst = p.partial + (size_t)g * (BM * BN);
     dst_m0 = 0;
     dst_n0 = 0;
@@ -397,6 +399,13 @@ __global__ __launch_bounds__(64 * kWaves) void w4a16_gemm_kernel(W4A16Params p) 
           }
           const size_t off = (size_t)m * dst_N + n;
           const int st = dst_dtype == kBF16AsF16 ? (int)kF16 : dst_dtype;  // storage dtype
+          if (resid) {  // gated residual on the rounded outputs (uniform over the workgroup)
+            const size_t goff = (size_t)(m / p.gate_rows) * dst_N + n;
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (n + e < dst_N)
+                v[e] = read_elem(resid, st, off + e) + read_elem(p.gate, st, goff + e) * round_to(st, v[e]);
+          }
           if (vec && n + 3 < dst_N) {
             if (st == kF32) {
               *(f32x4*)((float*)dst + off) = f32x4{v[0], v[1], v[2], v[3]};
@@ -471,6 +480,9 @@ __global__ __launch_bounds__(256) void w4a16_reduce_kernel(W4A16Params p, int BM
     float out = v[e] * rs * cu[e] + bv;
     if (p.act == kActGeluTanh) out = gelu_tanh(round_to(rnd, out));
     if (as_f16) out = round_to(kBF16, out) * rdown;  // exact in fp16
+    if (p.residual)  // gated residual on the rounded output
+      out = read_elem(p.residual, rnd, (size_t)m * p.N + n) +
+            read_elem(p.gate, rnd, (size_t)(m / p.gate_rows) * p.N + n) * round_to(rnd, out);
     write_elem(p.y, as_f16 ? (int)kF16 : p.out_dtype, (size_t)m * p.N + n, out);
   }
 }

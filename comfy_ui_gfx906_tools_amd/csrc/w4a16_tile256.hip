@@ -376,6 +376,9 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W
   }
 
   // ---- epilogue ----------------------------------------------------------------------------
+  // The gated residual epilogue is not built into variant 2 (4 waves of 256 x 64), whose
+  // accumulators leave no registers for it; the C ABI rejects it there.
+  constexpr bool kResidual = !(kWavesM == 1 && kWavesN == 4);
   // v = acc * row_scale * col_scale + bias (both scales exact powers of two); with the GELU
   // epilogue v is first rounded to the output dtype
   // (the unfused sequence's linear output) and then passed through gelu_tanh. Bias and row
@@ -468,6 +471,13 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W
 #pragma unroll
             for (int e = 0; e < 4; ++e) v[e] = value(i, j, bq, e);
             const size_t off = (size_t)m * N + n;
+            if (kResidual && p.residual) {  // gated residual (uniform over the workgroup)
+              const float* rp = (const float*)p.residual + off;
+              const float* gp = (const float*)p.gate + (size_t)(m / p.gate_rows) * N + n;
+#pragma unroll
+              for (int e = 0; e < 4; ++e)
+                if (n + e < N) v[e] = rp[e] + gp[e] * v[e];
+            }
             if (vec && n + 3 < N) {
               *(f32x4*)((float*)p.y + off) = f32x4{v[0], v[1], v[2], v[3]};
             } else {
@@ -491,6 +501,7 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W
       wait_lgkm();
       barrier_no_fence();
       const bool vec = (N % 8) == 0 && (((uintptr_t)p.y) & 15) == 0;
+      const bool rvec = vec && ((((uintptr_t)p.residual) | ((uintptr_t)p.gate)) & 15) == 0;
       static_for<0, 2>([&](auto hc) {
         constexpr int half = decltype(hc)::value;
         static_for<0, WM>([&](auto jc) {
@@ -519,10 +530,15 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W
         for (int k = 0; k < kHalfRows * kChunks / (64 * kWaves); ++k) {
           const int q = threadIdx.x + k * 64 * kWaves;
           const int r = q / kChunks, c = q % kChunks;
-          const u32x4 v = *(const u32x4*)(lds + r * (BN * 2) + ((c ^ (r & 31)) << 4));
+          u32x4 v = *(const u32x4*)(lds + r * (BN * 2) + ((c ^ (r & 31)) << 4));
           const int m = m0 + half * kHalfRows + r, n = n0 + 8 * c;
           if (m < M && n < N) {
             uint16_t* dst = (uint16_t*)p.y + (size_t)m * N + n;
+            if constexpr ((kOdt == kBF16 || kOdt == kF16) && kResidual) {
+              if (p.residual)  // gated residual on the rounded outputs (uniform over the workgroup)
+                v = gated_residual8<kOdt>(v, (const uint16_t*)p.residual + (size_t)m * N + n,
+                                          (const uint16_t*)p.gate + (size_t)(m / p.gate_rows) * N + n, min(8, N - n), rvec);
+            }
             if (vec && n + 8 <= N) {
               *(u32x4*)dst = v;
             } else {

@@ -115,13 +115,16 @@ def _scales_kn(layer, ws: torch.Tensor, rows: slice | None):
     return kn
 
 
-def _linear(layer, x, gelu: bool = False, rows: slice | None = None, staged_out: bool = False):
+def _linear(layer, x, gelu: bool = False, rows: slice | None = None, staged_out: bool = False,
+            residual: tuple | None = None):
     """layer(x), optionally followed by GELU-tanh, optionally restricted to output rows `rows`
     of the weight. Engine layers fuse the GELU into the GEMM epilogue, take row slices of
     weight_q4 / weight_scale / bias as views (rows of the packed layout are contiguous) and
     accept a Staged operand. staged_out: return the bf16 result as the next GEMM's Staged operand
     (row-scaled fp16 written by this GEMM's epilogue, no staging pass) where the engine can: an
-    engine layer without rotation or row slice, a Staged bf16 input; otherwise a plain tensor."""
+    engine layer without rotation or row slice, a Staged bf16 input; otherwise a plain tensor.
+    residual = (r, gate, inplace): return r + gate * layer(x) for r [B, L, N] and gate [B, 1, N]
+    (into r itself when inplace), fused into the GEMM epilogue on engine layers."""
     if _is_engine_linear(layer):
         wq, ws, b = layer.weight_q4, layer.weight_scale, layer.bias
         # the fp16 dequant's per-column factors, kept with the whole weight (rows slice them), and
@@ -132,18 +135,25 @@ def _linear(layer, x, gelu: bool = False, rows: slice | None = None, staged_out:
             wq, ws = wq[rows], ws[rows]
             b = b[rows] if b is not None else None
             cs = cs[rows] if cs is not None else None
+        N = wq.shape[0]
+        rk, lead = {}, None
+        if residual is not None:  # the gated residual in the epilogue: y = r + gate * linear
+            r, gate, inplace = residual
+            lead = r.shape[:-1]
+            r2 = r.reshape(-1, N)
+            rk = dict(residual=r2, gate=gate.reshape(-1, N), out=r2 if inplace else None)
         if isinstance(x, Staged):
             if layer.rotation_group:
                 raise RuntimeError("a layer with activation rotation takes a plain activation tensor")
             bias = b.to(x.dtype) if b is not None else None
-            if staged_out and rows is None and x.dtype == torch.bfloat16:
+            if staged_out and rows is None and x.dtype == torch.bfloat16 and residual is None:
                 y16, rs = _lib.w4a16_gemm(x.x16, wq, ws, bias, out_dtype=x.dtype, row_scale=x.row_scale, gelu=gelu,
                                           col_scale=cs, scales_kn=kn, f16_rowscaled=True,
                                           out_bound=_lib.cached_out_bound(wq, ws, bias))
                 return Staged(y16, rs, x.lead, x.dtype)
             y = _lib.w4a16_gemm(x.x16, wq, ws, bias, out_dtype=x.dtype, row_scale=x.row_scale, gelu=gelu,
-                                col_scale=cs, scales_kn=kn)
-            return y.reshape(*x.lead, wq.shape[0])
+                                col_scale=cs, scales_kn=kn, **rk)
+            return y.reshape(*(lead if lead is not None else x.lead), N)
         shape = x.shape
         x2 = x.reshape(-1, shape[-1])
         bias = b.to(x.dtype) if b is not None else None
@@ -152,17 +162,21 @@ def _linear(layer, x, gelu: bool = False, rows: slice | None = None, staged_out:
             if shape[-1] <= ROTATE_FUSED_MAX_K:
                 x16, rs = _lib.rotate_rows_to_f16(x2, get_group_signs(g, x2.device), g)
                 y = _lib.w4a16_gemm(x16, wq, ws, bias, out_dtype=x.dtype, row_scale=rs, gelu=gelu, col_scale=cs,
-                                    scales_kn=kn)
-                return y.reshape(*shape[:-1], wq.shape[0])
+                                    scales_kn=kn, **rk)
+                return y.reshape(*shape[:-1], N)
             x2 = apply_group_rotation(x2.float(), get_group_rotation(shape[-1], g, x2.device), g)
-        y = _lib.w4a16_gemm(x2, wq, ws, bias, out_dtype=x.dtype, gelu=gelu, col_scale=cs, scales_kn=kn)
-        return y.reshape(*shape[:-1], wq.shape[0])
+        y = _lib.w4a16_gemm(x2, wq, ws, bias, out_dtype=x.dtype, gelu=gelu, col_scale=cs, scales_kn=kn, **rk)
+        return y.reshape(*shape[:-1], N)
     w, b = layer.weight, layer.bias
     if rows is not None:
         w = w[rows]
         b = b[rows] if b is not None else None
     y = F.linear(x, w.to(x.dtype), b.to(x.dtype) if b is not None else None)
-    return F.gelu(y, approximate="tanh") if gelu else y
+    y = F.gelu(y, approximate="tanh") if gelu else y
+    if residual is not None:
+        r, gate, inplace = residual
+        return r.add_(gate * y) if inplace else r + gate * y
+    return y
 
 
 def timestep_embedding(t: torch.Tensor, dim: int, max_period: float = 10000.0, time_factor: float = 1000.0):
@@ -245,14 +259,6 @@ def _adaln(x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor) -> Staged:
     else:
         x16, rs = torch.cat([p[0] for p in parts]), torch.cat([p[1] for p in parts])
     return Staged(x16, rs, (B, L), x.dtype)
-
-
-def _residual(x: torch.Tensor, gate: torch.Tensor, y: torch.Tensor, inplace: bool = False) -> torch.Tensor:
-    """x + gate * y for x, y [B, L, K] and gate [B, 1, K]; into x itself when inplace."""
-    out = x if inplace else torch.empty_like(x)
-    for b in range(x.shape[0]):
-        _lib.gated_residual(x[b], gate[b].reshape(-1), y[b], out=out[b])
-    return out
 
 
 def _heads_into(attn: "SelfAttention", qkv: torch.Tensor, cos, sin, q, k, v, l_offset: int) -> None:
@@ -364,13 +370,14 @@ class DoubleStreamBlock(torch.nn.Module):
         _heads_into(self.txt_attn, _linear(self.txt_attn.qkv, _adaln(txt, t_sh1, t_sc1)), cos, sin, q, k, v, 0)
         _heads_into(self.img_attn, _linear(self.img_attn.qkv, _adaln(img, i_sh1, i_sc1)), cos, sin, q, k, v, n_txt)
         o = _sdpa_heads(q, k, v)
-        img = _residual(img, i_g1, _linear(self.img_attn.proj, _heads_staged(o, n_txt, n_img)))
+        # gated residuals in the proj / fc2 epilogues; the block's inputs stay untouched
+        img = _linear(self.img_attn.proj, _heads_staged(o, n_txt, n_img), residual=(img, i_g1, False))
         # fc1 writes its GELU output straight as fc2's fp16 operand (no staging pass between them)
         h = _linear(self.img_mlp[0], _adaln(img, i_sh2, i_sc2), gelu=True, staged_out=True)
-        img = _residual(img, i_g2, _linear(self.img_mlp[2], h), inplace=True)
-        txt = _residual(txt, t_g1, _linear(self.txt_attn.proj, _heads_staged(o, 0, n_txt)))
+        img = _linear(self.img_mlp[2], h, residual=(img, i_g2, True))
+        txt = _linear(self.txt_attn.proj, _heads_staged(o, 0, n_txt), residual=(txt, t_g1, False))
         h = _linear(self.txt_mlp[0], _adaln(txt, t_sh2, t_sc2), gelu=True, staged_out=True)
-        txt = _residual(txt, t_g2, _linear(self.txt_mlp[2], h), inplace=True)
+        txt = _linear(self.txt_mlp[2], h, residual=(txt, t_g2, True))
         return img, txt
 
 
@@ -411,8 +418,9 @@ class SingleStreamBlock(torch.nn.Module):
                               self.norm.query_norm.scale, self.norm.key_norm.scale, cos[b, 0], sin[b, 0], self.heads,
                               out=(q[b], k[b], v[b]))
         mlp = _linear(self.linear1, st, gelu=True, rows=slice(h3, None))
-        # linear2's input [attention | gelu(mlp)] gathered straight into its fp16 operand
-        return _residual(x, gate, _linear(self.linear2, _heads_staged(_sdpa_heads(q, k, v), 0, L, mlp)))
+        # linear2's input [attention | gelu(mlp)] gathered straight into its fp16 operand, the gated
+        # residual in its epilogue
+        return _linear(self.linear2, _heads_staged(_sdpa_heads(q, k, v), 0, L, mlp), residual=(x, gate, False))
 
 
 class LastLayer(torch.nn.Module):

@@ -46,7 +46,7 @@ enum qlinear_status {
 const char* qlinear_last_error(void);
 
 /* ABI version of this header: (major << 16) | minor. 2.0: qlinear_w4a16_gemm takes col_scale;
- * 3.0: qlinear_w4a16_gemm(_noalloc) take w_scale_kn. */
+ * 3.0: qlinear_w4a16_gemm(_noalloc) take w_scale_kn; 4.0: and residual. */
 int qlinear_abi_version(void);
 
 /* ---------------------------------------------------------------------------------------
@@ -95,6 +95,21 @@ int qlinear_abi_version(void);
  * automatic plan never picks another). No counterpart in the reference, whose linears each read
  * and write their activations. */
 #define QL_W4A16_F16_ROWSCALED 4
+/* flags bit: gated residual epilogue, y = residual + gate[m / gate_rows] (.) v, where v is the
+ * output as it would otherwise be stored (bias, activation, rounded to out_dtype) and the sum is
+ * formed in fp32 (the product of two 16-bit numbers is exact there) and rounded to out_dtype: the
+ * result of this GEMM followed by the elementwise kernel x + gate * y, in one pass (a DiT block's
+ * "x = x + gate * linear(h)"). residual [M, N] and gate [ceil(M / gate_rows), N] have out_dtype,
+ * aligned to their elements; y may be residual itself (in place), any other overlap is undefined.
+ * Described by the ql_w4a16_residual passed as `residual` (NULL without this flag). Not with
+ * QL_W4A16_F16_ROWSCALED; tile kernels 0-5 only (the automatic plan picks no other). No
+ * counterpart in the reference, whose linears end at the bias. */
+#define QL_W4A16_GATED_RESIDUAL 16
+typedef struct ql_w4a16_residual {
+  const void* residual; /* [M, N], out_dtype */
+  const void* gate;     /* [ceil(M / gate_rows), N], out_dtype */
+  int64_t gate_rows;    /* output rows per gate row: M for one gate row, L for [B, L, N] outputs */
+} ql_w4a16_residual;
 /* flags bits 8-11: 0 = automatic kernel choice, c + 1 = force kernel configuration c
  * (0-3: 256 / 128 / 64 / 16-row x 256-column tiles, 4 waves; 4-6: 256 x 256 tiles with 8 waves
  * as 2 x 4, 8 waves as 1 x 8, 4 waves as 1 x 4, K % 64 == 0, whole tiles only; 7: M <= 4,
@@ -113,8 +128,9 @@ size_t qlinear_w4a16_workspace_bytes(int x_dtype, int64_t M, int64_t N, int64_t 
 int qlinear_w4a16_gemm(int x_dtype, int out_dtype, const void* x, const float* row_scale,
                        const void* w_q4, const float* w_scale, const float* w_scale_kn,
                        const float* col_scale, const void* bias, void* y, const float* out_bound,
-                       float* out_row_scale, int64_t M, int64_t N, int64_t K, int splits, int flags,
-                       void* workspace, size_t workspace_bytes, void* stream);
+                       float* out_row_scale, const ql_w4a16_residual* residual, int64_t M,
+                       int64_t N, int64_t K, int splits, int flags, void* workspace,
+                       size_t workspace_bytes, void* stream);
 
 /* Group-major copy of the group scales: w_scale_kn[g * N + n] = w_scale[n * (K/32) + g]
  * ([K/32, N] fp32, N * K / 8 bytes). Passed as w_scale_kn to qlinear_w4a16_gemm (NULL there =
@@ -151,8 +167,9 @@ int qlinear_w4a16_out_bound(const void* w_q4, const float* w_scale, const void* 
 int qlinear_w4a16_gemm_noalloc(int x_dtype, int out_dtype, const void* x, const float* row_scale,
                                const void* w_q4, const float* w_scale, const float* w_scale_kn,
                                const float* col_scale, const void* bias, void* y,
-                               const float* out_bound, float* out_row_scale, int64_t M, int64_t N,
-                               int64_t K, int splits, int flags, void* stream);
+                               const float* out_bound, float* out_row_scale,
+                               const ql_w4a16_residual* residual, int64_t M, int64_t N, int64_t K,
+                               int splits, int flags, void* stream);
 
 /* Column factors of the fp16 dequant: col_scale[n] = 2^e_n with 8 * max_g |w_scale[n, g]| * 2^-e_n
  * in [2^14, 2^15) (e_n clamped to [-126, 126]; 1 for a column whose scales are all 0 or not

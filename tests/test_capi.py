@@ -39,7 +39,7 @@ def lib():
 def test_header_parses():
     fns = _header_functions()
     assert {"qlinear_w4a16_gemm", "qlinear_w8a8_gemm", "qlinear_quantize_int4", "qlinear_last_error"} <= set(fns)
-    assert fns["qlinear_w4a16_gemm"] == 20 and fns["qlinear_abi_version"] == 0
+    assert fns["qlinear_w4a16_gemm"] == 21 and fns["qlinear_abi_version"] == 0
 
 
 def test_every_declared_symbol_is_exported(lib):
@@ -61,7 +61,7 @@ def test_ctypes_table_matches_header(lib):
 
 
 def test_abi_version_and_error_text(lib):
-    assert lib.qlinear_abi_version() >> 16 == 3
+    assert lib.qlinear_abi_version() >> 16 == 4
     assert isinstance(lib.qlinear_last_error(), bytes)
 
 
@@ -70,8 +70,8 @@ def _err(lib):
 
 
 def test_w4a16_argument_checks(lib):
-    def f(*a):  # every argument but w_scale_kn (NULL: the checks below do not depend on it)
-        return lib.qlinear_w4a16_gemm(*a[:6], None, *a[6:])
+    def f(*a):  # every argument but w_scale_kn and residual (NULL: the checks below do not use them)
+        return lib.qlinear_w4a16_gemm(*a[:6], None, *a[6:11], None, *a[11:])
     # bad activation dtype (int32)
     assert f(3, 0, None, None, None, None, None, None, None, None, None, 4, 64, 64, 0, 0, None, 0, None) == QL_ERR_DTYPE
     assert "x dtype" in _err(lib)
@@ -117,6 +117,27 @@ def test_w4a16_argument_checks(lib):
         assert f(2, 2, None, None, None, None, None, None, None, None, None, 0, 64, 128, 2, cfg(c), None, 0, None) == QL_ERR_ARG
         assert "whole tiles" in _err(lib)
     assert f(2, 2, None, None, None, None, None, None, None, None, None, 0, 64, 128, 2, cfg(5), None, 0, None) == QL_OK
+
+
+def test_w4a16_gated_residual_argument_checks(lib):
+    from comfy_ui_gfx906_tools_amd import _lib
+    f = lib.qlinear_w4a16_gemm
+    P = ctypes.c_void_p(256)  # never dereferenced: every call below fails its checks first
+    res = _lib.Residual(256, 512, 4)
+    bad_rows = _lib.Residual(256, 512, 0)
+    odd = _lib.Residual(257, 512, 4)
+    GR = 16
+    args = lambda r, flags, od=2: (2, od, P, None, P, P, None, None, None, P, None, None, r, 8, 64, 64, 0, flags,  # noqa: E731
+                                   None, 0, None)
+    assert f(*args(None, GR)) == QL_ERR_ARG and "exactly when" in _err(lib)
+    assert f(*args(ctypes.addressof(res), 0)) == QL_ERR_ARG
+    assert f(*args(ctypes.addressof(bad_rows), GR)) == QL_ERR_ARG and "gate_rows" in _err(lib)
+    assert f(*args(ctypes.addressof(odd), GR)) == QL_ERR_ALIGN
+    assert f(*args(ctypes.addressof(res), GR | 4)) == QL_ERR_ARG and "do not combine" in _err(lib)
+    assert f(*args(ctypes.addressof(res), GR | (8 << 8))) == QL_ERR_ARG and "configurations 0-5" in _err(lib)
+    assert f(*args(ctypes.addressof(res), GR | (7 << 8))) == QL_ERR_ARG  # variant 2 of the 256 x 256 kernel
+    # host-side plan queries see the flag: the direct kernels are never planned with it
+    assert _lib.load_library().qlinear_check_launch_plan(0, 2, 8, 4096, 4096, 0, GR, 256) == 0
 
 
 def test_quantizer_and_w8a8_argument_checks(lib):
