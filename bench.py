@@ -60,6 +60,30 @@ def calibrate_copy():
     print(json.dumps({"copy_bytes": n, "launches": 3}), flush=True)
 
 
+def host_cpu() -> dict:
+    """The host CPU the cpu_baseline ran on: model name, logical CPUs visible to this process and
+    the vector ISA extensions the kernel reports (from /proc/cpuinfo, as lscpu shows them)."""
+    model, flags = "unknown", set()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                k, _, v = line.partition(":")
+                k = k.strip()
+                if k == "model name" and model == "unknown":
+                    model = v.strip()
+                elif k == "flags" and not flags:
+                    flags = set(v.split())
+    except OSError:
+        pass
+    isa = [f for f in ("sse4_2", "avx", "avx2", "fma", "avx512f", "avx512bw", "avx512vl", "avx512_vnni", "avx512_bf16",
+                       "avx_vnni", "amx_tile", "amx_bf16", "amx_int8") if f in flags]
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        usable = os.cpu_count() or 1
+    return {"model": model, "logical_cpus": usable, "isa": isa}
+
+
 def gelu_tanh_np(h):
     import numpy as np
     return 0.5 * h * (1.0 + np.tanh(np.float32(0.7978845608028654) * (h + np.float32(0.044715) * h * h * h)))
@@ -91,7 +115,7 @@ def cpu_baseline(x_bf16, w1, s1, b1, w2, s2, b2, repeats):
     flops = 2.0 * M_TOKENS * HIDDEN * MLP * 2
     return {"value": round(flops / best / 1e12, 4), "unit": "TFLOP/s", "cores": int(threads), "kind": "port",
             "sample": f"full C2 step on the host (M={M_TOKENS}, fp32 numpy BLAS, dequant outside the timing), "
-                      f"best of {repeats}: {best:.2f} s/step", "_check": float(np.abs(y).max())}
+                      f"best of {repeats}: {best:.2f} s/step", "cpu": host_cpu(), "_check": float(np.abs(y).max())}
 
 
 def main():
@@ -304,18 +328,53 @@ def bench_c3(args):
                         "unit": "TOP/s", "frac": round(ops / (gemm_ms * 1e-3) / 1e12 / PEAK_INT8_TOPS, 4),
                         "kernel": "w8a8_tile256_kernel", "avg_launch_ms": round(gemm_ms, 4)},
            "parity": {"int32_accumulators_exact": exact, "bf16_epilogue_exact": same, "pass": exact and same}}
+    # the producer fusion: in the single-stream block this linear's input is the adaLN of the
+    # residual stream; fused, the adaLN kernel writes the int8 operand and its scales itself
+    shift = (torch.randn(K, device="cuda", generator=g) * 0.3).to(torch.bfloat16)
+    scale = (torch.randn(K, device="cuda", generator=g) * 0.3).to(torch.bfloat16)
+
+    def unfused():
+        q, s = _lib.quantize_int8_per_token(_lib.adaln_modulate(x, shift, scale, out="plain"))
+        return _lib.w8a8_gemm(q, s, wq, sw, out_dtype=torch.bfloat16)
+
+    def fused():
+        q, s = _lib.adaln_modulate(x, shift, scale, out="i8")
+        return _lib.w8a8_gemm(q, s, wq, sw, out_dtype=torch.bfloat16)
+
+    same_fused = bool(torch.equal(unfused(), fused()))
+    times = {}
+    for name, fn in (("unfused", unfused), ("fused", fused)):
+        for _ in range(3):
+            fn()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(args.steps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        times[name] = e0.elapsed_time(e1) / args.steps
+    out["producer_fusion"] = {"step": "adaLN(x) -> per-token int8 -> W8A8 GEMM (bf16 out)",
+                              "unfused_ms": round(times["unfused"], 4), "fused_ms": round(times["fused"], 4),
+                              "saved_ms": round(times["unfused"] - times["fused"], 4), "bit_identical": same_fused}
     if not args.no_cpu_baseline:
-        # the oracle's exact integer matmul (int64 numpy) on a bounded sample of rows, scaled
+        # the oracle's exact integer matmul over the whole call: int8 codes in float64 (every
+        # partial sum is an integer below 2^53, so the products and sums are exact), numpy BLAS
+        # on all the host's cores, rows in chunks
+        import numpy as np
         from oracle import qlinear_oracle as orc
-        rows = 64
-        a = xq[:rows].cpu().numpy()
+        threads = torch.get_num_threads()
+        a = xq.cpu().numpy()
         b = wq.cpu().numpy()
         t0 = time.perf_counter()
-        orc.int8_matmul_exact(a, b)
+        acc64 = orc.int8_matmul_exact_f64(a, b)
         dt = time.perf_counter() - t0
-        out["cpu_baseline"] = {"value": round(2.0 * rows * N * K / dt / 1e12, 5), "unit": "TOP/s", "cores": 1,
-                               "kind": "port", "sample": f"oracle int8_matmul_exact on {rows} of {M} rows "
-                                                          f"(int64 numpy), {dt:.2f} s"}
+        ok = bool(np.array_equal(acc64[:64], orc.int8_matmul_exact(a[:64], b)))
+        out["cpu_baseline"] = {"value": round(ops / dt / 1e12, 5), "unit": "TOP/s", "cores": threads,
+                               "kind": "port", "sample": f"oracle int8_matmul_exact_f64 over the whole call ({M} rows, "
+                                                         f"float64 numpy BLAS, {threads} threads), {dt:.2f} s; "
+                                                         f"equals the int64 oracle on the first 64 rows: {ok}",
+                               "cpu": host_cpu()}
     print(json.dumps(out), flush=True)
 
 
@@ -460,7 +519,8 @@ def bench_c1(args):
             best = min(best, time.perf_counter() - t0)
         out["cpu_baseline"] = {"value": round(flops / best / 1e12, 4), "unit": "TFLOP/s", "cores": threads,
                                "kind": "port", "sample": f"whole C1 call, fp32 numpy BLAS on the host, dequant outside "
-                                                         f"the timing, best of {args.cpu_repeats}: {best:.3f} s"}
+                                                         f"the timing, best of {args.cpu_repeats}: {best:.3f} s",
+                               "cpu": host_cpu()}
     print(json.dumps(out), flush=True)
 
 
@@ -567,7 +627,7 @@ def bench_c5(args):
                             "sample": f"double block 0 ({t_double:.2f} s) and single block 0 ({t_single:.2f} s) in "
                                       f"fp32 torch on the host with the dequantized weights, extrapolated x"
                                       f"{cfg.depth_double} / x{cfg.depth_single} (embedders and final layer "
-                                      f"left out)"}}
+                                      f"left out)", "cpu": host_cpu()}}
     print(json.dumps(out), flush=True)
 
 

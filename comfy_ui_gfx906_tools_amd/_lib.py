@@ -62,6 +62,8 @@ SIGNATURES = {
     "qlinear_w8a8_gemm": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp]),
     "qlinear_adaln_modulate_f16": (_c_int, [_c_int, _c_vp, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64,
                                             ctypes.c_float, _c_vp]),
+    "qlinear_adaln_modulate": (_c_int, [_c_int, _c_int, _c_vp, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64,
+                                        ctypes.c_float, _c_vp]),
     "qlinear_qk_norm_rope": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64,
                                       _c_i64, _c_i64, _c_i64, ctypes.c_float, _c_vp]),
     "qlinear_w4a4_gemm": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int,
@@ -697,6 +699,40 @@ def adaln_modulate_f16(x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor
                                             float(eps), _stream_ptr(x.device))
     _check(rc, "adaln_modulate_f16")
     return x16, rs
+
+
+ADALN_F16_ROWSCALED, ADALN_PLAIN, ADALN_I8_PER_TOKEN = 0, 1, 2
+
+
+def adaln_modulate(x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor, out: str = "f16",
+                   eps: float = 1e-6):
+    """LayerNorm(x) * (1 + scale) + shift for x [M, K] (shift / scale [K]) written as `out`:
+    "f16" -> (x16 fp16 [M, K], row_scale fp32 [M]) as adaln_modulate_f16; "plain" -> the row in
+    x's dtype [M, K]; "i8" -> (q int8 [M, K], scale fp32 [M]), the W8A8 GEMM's per-token operand
+    (the plain output quantized by quantize_int8_per_token's rule, in the same pass)."""
+    lib = load_library()
+    kinds = {"f16": ADALN_F16_ROWSCALED, "plain": ADALN_PLAIN, "i8": ADALN_I8_PER_TOKEN}
+    if out not in kinds:
+        raise RuntimeError(f"out must be one of {sorted(kinds)}, got {out!r}")
+    x = _dev_tensor(x, "x")
+    shift = _dev_tensor(shift, "shift").reshape(-1)
+    scale = _dev_tensor(scale, "scale").reshape(-1)
+    if x.dim() != 2 or x.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+        raise RuntimeError(f"x must be a float [M, K] tensor, got {x.dtype} {tuple(x.shape)}")
+    M, K = x.shape
+    if shift.dtype != scale.dtype or shift.numel() != K or scale.numel() != K or shift.dtype == torch.int32:
+        raise RuntimeError(f"shift and scale must be float [{K}] tensors of one dtype, got {shift.dtype} "
+                           f"{tuple(shift.shape)} / {scale.dtype} {tuple(scale.shape)}")
+    odt = {"f16": torch.float16, "plain": x.dtype, "i8": torch.int8}[out]
+    y = torch.empty((M, K), dtype=odt, device=x.device)
+    rs = torch.empty((M,), dtype=torch.float32, device=x.device) if out != "plain" else None
+    with torch.cuda.device(x.device):
+        rc = lib.qlinear_adaln_modulate(kinds[out], _DTYPE_CODE[x.dtype], x.data_ptr(), _DTYPE_CODE[shift.dtype],
+                                        shift.data_ptr(), scale.data_ptr(), y.data_ptr(),
+                                        rs.data_ptr() if rs is not None else None, M, K, float(eps),
+                                        _stream_ptr(x.device))
+    _check(rc, "adaln_modulate")
+    return y if out == "plain" else (y, rs)
 
 
 def qk_norm_rope(qkv: torch.Tensor, q_norm: torch.Tensor, k_norm: torch.Tensor, cos: torch.Tensor,

@@ -820,8 +820,12 @@ int qlinear_w8a8_gemm(int out_dtype, const int8_t* xq, const float* x_scale, con
   return ok();
 }
 
-int qlinear_adaln_modulate_f16(int x_dtype, const void* x, int mod_dtype, const void* shift, const void* scale,
-                               void* x16, float* row_scale, int64_t M, int64_t K, float eps, void* stream) {
+int qlinear_adaln_modulate(int out_kind, int x_dtype, const void* x, int mod_dtype, const void* shift,
+                           const void* scale, void* out, float* row_scale, int64_t M, int64_t K, float eps,
+                           void* stream) {
+  if (out_kind != QL_ADALN_F16_ROWSCALED && out_kind != QL_ADALN_PLAIN && out_kind != QL_ADALN_I8_PER_TOKEN)
+    return fail(QL_ERR_ARG, "out_kind must be QL_ADALN_F16_ROWSCALED, QL_ADALN_PLAIN or QL_ADALN_I8_PER_TOKEN, got %d",
+                out_kind);
   if (x_dtype != QL_F32 && x_dtype != QL_F16 && x_dtype != QL_BF16)
     return fail(QL_ERR_DTYPE, "x dtype %s (%d) unsupported, expected float32/float16/bfloat16", dtype_name(x_dtype),
                 x_dtype);
@@ -833,14 +837,22 @@ int qlinear_adaln_modulate_f16(int x_dtype, const void* x, int mod_dtype, const 
                 (long long)K);
   if (!(eps >= 0.0f)) return fail(QL_ERR_ARG, "eps must be >= 0, got %g", (double)eps);
   if (M == 0) return ok();
-  if (!x || !shift || !scale || !x16 || !row_scale)
-    return fail(QL_ERR_ARG, "null x / shift / scale / x16 / row_scale pointer");
-  if (!aligned16(x) || !aligned16(shift) || !aligned16(scale) || !aligned16(x16))
-    return fail(QL_ERR_ALIGN, "x, shift, scale and x16 must be 16-byte aligned");
-  const hipError_t e = adaln_to_f16_launch(x_dtype, mod_dtype, x, shift, scale, x16, row_scale, M, K, eps,
-                                           (hipStream_t)stream);
-  if (e != hipSuccess) return fail(QL_ERR_LAUNCH, "adaln_modulate_f16 launch failed: %s", hipGetErrorString(e));
+  if (!x || !shift || !scale || !out || (out_kind != QL_ADALN_PLAIN && !row_scale))
+    return fail(QL_ERR_ARG, "null x / shift / scale / out / row_scale pointer");
+  if (!aligned16(x) || !aligned16(shift) || !aligned16(scale) ||
+      (out_kind == QL_ADALN_I8_PER_TOKEN ? ((uintptr_t)out & 7) != 0 : !aligned16(out)))
+    return fail(QL_ERR_ALIGN, "x, shift, scale and out must be 16-byte aligned (int8 out: 8-byte)");
+  const int kind = out_kind == QL_ADALN_PLAIN ? kAdalnPlain : out_kind == QL_ADALN_I8_PER_TOKEN ? kAdalnI8 : kAdalnF16;
+  const hipError_t e = adaln_launch(kind, x_dtype, mod_dtype, x, shift, scale, out, row_scale, M, K, eps,
+                                    (hipStream_t)stream);
+  if (e != hipSuccess) return fail(QL_ERR_LAUNCH, "adaln_modulate launch failed: %s", hipGetErrorString(e));
   return ok();
+}
+
+int qlinear_adaln_modulate_f16(int x_dtype, const void* x, int mod_dtype, const void* shift, const void* scale,
+                               void* x16, float* row_scale, int64_t M, int64_t K, float eps, void* stream) {
+  return qlinear_adaln_modulate(QL_ADALN_F16_ROWSCALED, x_dtype, x, mod_dtype, shift, scale, x16, row_scale, M, K, eps,
+                                stream);
 }
 
 int qlinear_qk_norm_rope(int dtype, const void* qkv, const void* q_norm, const void* k_norm, const float* cos_t,

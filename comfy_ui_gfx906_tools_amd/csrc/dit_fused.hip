@@ -4,7 +4,8 @@
 //
 //  * adaln_to_f16_kernel: LayerNorm (no affine) of a row, then (1 + scale) * y + shift, written
 //    as the row-scaled fp16 operand of the W4A16 GEMM (the format of rows_to_scaled_f16_kernel:
-//    max |y| * 2^-e in [2^14, 2^15) before the fp16 rounding, row_scale = 2^e).
+//    max |y| * 2^-e in [2^14, 2^15) before the fp16 rounding, row_scale = 2^e), as the plain row,
+//    or as the per-token int8 operand of the W8A8 GEMM.
 //  * qk_norm_rope_kernel: splits a qkv projection [L, 3, H, D] into q, k, v [H, L_out, D] at row
 //    offset l0, with RMSNorm over D (learned scale) and the RoPE pair rotation on q and k.
 //  * gated_residual_kernel: out = x + gate * y with gate broadcast over rows.
@@ -89,10 +90,14 @@ __device__ __forceinline__ float block_max(float v, float* red) {
 }
 
 // One 256-thread block per row; thread t holds elements 8t + 2048 r (r < R) in registers, so the
-// row is read from HBM once. K % 8 == 0, K <= 2048 R.
-template <int XDT, int MDT, int R>
+// row is read from HBM once. K % 8 == 0, K <= 2048 R. OUT: kAdalnF16 the row-scaled fp16 operand
+// of the W4A16 GEMM, kAdalnPlain the row in x's dtype, kAdalnI8 the per-token int8 operand of the
+// W8A8 GEMM: the row rounded to x's dtype, then quantized by qlinear_quantize_int8_per_token's
+// rule (s = fl(max(amax, 1e-8) * fl(1/127)), q = clamp(rint(v / s), -127, 127), IEEE division),
+// row_scale[m] = s.
+template <int XDT, int MDT, int R, int OUT>
 __global__ __launch_bounds__(256) void adaln_to_f16_kernel(const void* __restrict__ x, const void* __restrict__ shift,
-                                                           const void* __restrict__ scale, _Float16* __restrict__ x16,
+                                                           const void* __restrict__ scale, void* __restrict__ out,
                                                            float* __restrict__ row_scale, int K, float eps) {
   __shared__ float red[3][4];
   const size_t base = (size_t)blockIdx.x * K;
@@ -132,11 +137,39 @@ __global__ __launch_bounds__(256) void adaln_to_f16_kernel(const void* __restric
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         v[r][e] = (v[r][e] - mean) * rstd * (1.0f + sc[e]) + sh[e];
+        if constexpr (OUT == kAdalnI8) v[r][e] = round_to(XDT, v[r][e]);
         amax = fmaxf(amax, fabsf(v[r][e]));
       }
     }
   }
+  if constexpr (OUT == kAdalnPlain) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int k = threadIdx.x * 8 + r * 2048;
+      if (k < K) store8<XDT>(out, base + k, v[r]);
+    }
+    return;
+  }
   amax = block_max(amax, red[2]);
+  if constexpr (OUT == kAdalnI8) {
+    const float s = __fmul_rn(fmaxf(amax, 1e-8f), 1.0f / 127.0f);
+    if (threadIdx.x == 0) row_scale[blockIdx.x] = s;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int k = threadIdx.x * 8 + r * 2048;
+      if (k < K) {
+        uint32_t w[2] = {0u, 0u};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int c = (int)fminf(fmaxf(rintf(__fdiv_rn(v[r][e], s)), -127.0f), 127.0f);
+          w[e >> 2] |= ((uint32_t)c & 0xFFu) << (8 * (e & 3));
+        }
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        *(u32x2*)((int8_t*)out + base + k) = u32x2{w[0], w[1]};
+      }
+    }
+    return;
+  }
   int ex = 0;
   if (amax > 0.0f && amax <= 3.0e38f) {
     int E;
@@ -151,7 +184,7 @@ __global__ __launch_bounds__(256) void adaln_to_f16_kernel(const void* __restric
       float o[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] = ldexpf(v[r][e], -ex);
-      store8<kF16>(x16, base + k, o);
+      store8<kF16>(out, base + k, o);
     }
   }
 }
@@ -252,43 +285,55 @@ __global__ __launch_bounds__(256) void heads_to_f16_kernel(const void* __restric
   }
 }
 
-template <int XDT, int MDT>
-hipError_t adaln_launch_r(const void* x, const void* shift, const void* scale, void* x16, float* rs, int64_t M,
+template <int XDT, int MDT, int OUT>
+hipError_t adaln_launch_r(const void* x, const void* shift, const void* scale, void* out, float* rs, int64_t M,
                           int64_t K, float eps, hipStream_t st) {
   const dim3 grid((unsigned)M), block(256);
   if (K <= 2048)
-    hipLaunchKernelGGL((adaln_to_f16_kernel<XDT, MDT, 1>), grid, block, 0, st, x, shift, scale, (_Float16*)x16, rs,
-                       (int)K, eps);
+    hipLaunchKernelGGL((adaln_to_f16_kernel<XDT, MDT, 1, OUT>), grid, block, 0, st, x, shift, scale, out, rs, (int)K,
+                       eps);
   else if (K <= 4096)
-    hipLaunchKernelGGL((adaln_to_f16_kernel<XDT, MDT, 2>), grid, block, 0, st, x, shift, scale, (_Float16*)x16, rs,
-                       (int)K, eps);
+    hipLaunchKernelGGL((adaln_to_f16_kernel<XDT, MDT, 2, OUT>), grid, block, 0, st, x, shift, scale, out, rs, (int)K,
+                       eps);
   else if (K <= 8192)
-    hipLaunchKernelGGL((adaln_to_f16_kernel<XDT, MDT, 4>), grid, block, 0, st, x, shift, scale, (_Float16*)x16, rs,
-                       (int)K, eps);
+    hipLaunchKernelGGL((adaln_to_f16_kernel<XDT, MDT, 4, OUT>), grid, block, 0, st, x, shift, scale, out, rs, (int)K,
+                       eps);
   else
-    hipLaunchKernelGGL((adaln_to_f16_kernel<XDT, MDT, 8>), grid, block, 0, st, x, shift, scale, (_Float16*)x16, rs,
-                       (int)K, eps);
+    hipLaunchKernelGGL((adaln_to_f16_kernel<XDT, MDT, 8, OUT>), grid, block, 0, st, x, shift, scale, out, rs, (int)K,
+                       eps);
   return hipGetLastError();
 }
 
-template <int XDT>
-hipError_t adaln_launch_x(int mod_dtype, const void* x, const void* shift, const void* scale, void* x16, float* rs,
+template <int XDT, int OUT>
+hipError_t adaln_launch_x(int mod_dtype, const void* x, const void* shift, const void* scale, void* out, float* rs,
                           int64_t M, int64_t K, float eps, hipStream_t st) {
   switch (mod_dtype) {
-    case kF32: return adaln_launch_r<XDT, kF32>(x, shift, scale, x16, rs, M, K, eps, st);
-    case kF16: return adaln_launch_r<XDT, kF16>(x, shift, scale, x16, rs, M, K, eps, st);
-    default: return adaln_launch_r<XDT, kBF16>(x, shift, scale, x16, rs, M, K, eps, st);
+    case kF32: return adaln_launch_r<XDT, kF32, OUT>(x, shift, scale, out, rs, M, K, eps, st);
+    case kF16: return adaln_launch_r<XDT, kF16, OUT>(x, shift, scale, out, rs, M, K, eps, st);
+    default: return adaln_launch_r<XDT, kBF16, OUT>(x, shift, scale, out, rs, M, K, eps, st);
+  }
+}
+
+template <int OUT>
+hipError_t adaln_launch_o(int x_dtype, int mod_dtype, const void* x, const void* shift, const void* scale, void* out,
+                          float* row_scale, int64_t M, int64_t K, float eps, hipStream_t stream) {
+  switch (x_dtype) {
+    case kF32: return adaln_launch_x<kF32, OUT>(mod_dtype, x, shift, scale, out, row_scale, M, K, eps, stream);
+    case kF16: return adaln_launch_x<kF16, OUT>(mod_dtype, x, shift, scale, out, row_scale, M, K, eps, stream);
+    default: return adaln_launch_x<kBF16, OUT>(mod_dtype, x, shift, scale, out, row_scale, M, K, eps, stream);
   }
 }
 
 }  // namespace
 
-hipError_t adaln_to_f16_launch(int x_dtype, int mod_dtype, const void* x, const void* shift, const void* scale,
-                               void* x16, float* row_scale, int64_t M, int64_t K, float eps, hipStream_t stream) {
-  switch (x_dtype) {
-    case kF32: return adaln_launch_x<kF32>(mod_dtype, x, shift, scale, x16, row_scale, M, K, eps, stream);
-    case kF16: return adaln_launch_x<kF16>(mod_dtype, x, shift, scale, x16, row_scale, M, K, eps, stream);
-    default: return adaln_launch_x<kBF16>(mod_dtype, x, shift, scale, x16, row_scale, M, K, eps, stream);
+hipError_t adaln_launch(int out_kind, int x_dtype, int mod_dtype, const void* x, const void* shift, const void* scale,
+                        void* out, float* row_scale, int64_t M, int64_t K, float eps, hipStream_t stream) {
+  switch (out_kind) {
+    case kAdalnF16: return adaln_launch_o<kAdalnF16>(x_dtype, mod_dtype, x, shift, scale, out, row_scale, M, K, eps, stream);
+    case kAdalnPlain:
+      return adaln_launch_o<kAdalnPlain>(x_dtype, mod_dtype, x, shift, scale, out, row_scale, M, K, eps, stream);
+    case kAdalnI8: return adaln_launch_o<kAdalnI8>(x_dtype, mod_dtype, x, shift, scale, out, row_scale, M, K, eps, stream);
+    default: return hipErrorInvalidValue;
   }
 }
 

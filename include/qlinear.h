@@ -306,6 +306,23 @@ int qlinear_adaln_modulate_f16(int x_dtype, const void* x, int mod_dtype, const 
                                const void* scale, void* x16, float* row_scale, int64_t M,
                                int64_t K, float eps, void* stream);
 
+/* The same adaLN row y written as out_kind says:
+ *   QL_ADALN_F16_ROWSCALED  as qlinear_adaln_modulate_f16 (out = x16 fp16, row_scale = 2^e_m);
+ *   QL_ADALN_PLAIN          y rounded to x's dtype, out [M, K] of that dtype (row_scale unused);
+ *   QL_ADALN_I8_PER_TOKEN   the W8A8 GEMM's operand: y rounded to x's dtype, then quantized as
+ *                           qlinear_quantize_int8_per_token quantizes it (out int8 [M, K],
+ *                           row_scale[m] = the token's scale) -- the PLAIN output followed by
+ *                           that quantizer, bit for bit, without the round trip of the bf16 row
+ *                           through HBM (the reference quantizes in a launch of its own,
+ *                           ops.py:181, csrc/int8_gemm.hip:215-246).
+ * out 16-byte aligned (8-byte for int8). */
+#define QL_ADALN_F16_ROWSCALED 0
+#define QL_ADALN_PLAIN 1
+#define QL_ADALN_I8_PER_TOKEN 2
+int qlinear_adaln_modulate(int out_kind, int x_dtype, const void* x, int mod_dtype,
+                           const void* shift, const void* scale, void* out, float* row_scale,
+                           int64_t M, int64_t K, float eps, void* stream);
+
 /* QK-norm + RoPE + head split of a qkv projection [L, 3, H, D] (q, k, v blocks of H heads):
  * q[h, l_offset + l, :] = rope(rmsnorm(q_in[l, h, :]) * q_norm), likewise k with k_norm,
  * v[h, l_offset + l, :] = v_in[l, h, :]; q, k, v are [H, L_out, D] (the attention layout), so

@@ -231,6 +231,21 @@ def int8_matmul_exact(a: np.ndarray, b: np.ndarray) -> np.ndarray:
     return np.asarray(a, dtype=np.int64) @ np.asarray(b, dtype=np.int64).T
 
 
+def int8_matmul_exact_f64(a: np.ndarray, b: np.ndarray, chunk: int = 512) -> np.ndarray:
+    """int8_matmul_exact through float64 BLAS (all the host's cores): int8 codes are exact in
+    float64 and every partial sum of K products stays below 127 * 128 * K < 2^53 for K < 2^38, so
+    each product and sum is exact and the result equals the int64 matmul. Rows in chunks to bound
+    the float64 copies. Returns int64."""
+    a = np.asarray(a)
+    bt = np.asarray(b, dtype=np.float64).T
+    if a.shape[1] >= (1 << 38):
+        raise ValueError("K too large for an exact float64 accumulation")
+    out = np.empty((a.shape[0], bt.shape[1]), dtype=np.int64)
+    for r in range(0, a.shape[0], chunk):
+        out[r:r + chunk] = (a[r:r + chunk].astype(np.float64) @ bt).astype(np.int64)
+    return out
+
+
 def w8a8_epilogue(acc: np.ndarray, sx: np.ndarray, sw: np.ndarray, bias: np.ndarray | None = None) -> np.ndarray:
     """float(acc) * (sx[m] * sw[n]) (+ bias[n]), each operation rounded in fp32 -- the order of
     int8_gemm.hip:191-193 (fmaf(float(ip), as * bs, 0)) and :209 (v += bias). Returns fp32."""

@@ -324,6 +324,18 @@ def test_int8_matmul_exact_bruteforce():
     assert orc.int8_matmul_exact(big, big)[0, 0] == 12288 * 127 * 127
 
 
+def test_int8_matmul_exact_f64_equals_int64():
+    """The float64-BLAS form is exact: equal to the int64 matmul (itself pinned by brute force
+    above) on random codes, on the extreme codes at large K, and across its row chunks."""
+    rng = np.random.default_rng(13)
+    a = rng.integers(-128, 128, (70, 3072), dtype=np.int16).astype(np.int8)
+    b = rng.integers(-128, 128, (33, 3072), dtype=np.int16).astype(np.int8)
+    assert np.array_equal(orc.int8_matmul_exact_f64(a, b, chunk=16), orc.int8_matmul_exact(a, b))
+    big = np.full((2, 65536), -128, np.int8)
+    got = orc.int8_matmul_exact_f64(big, big)
+    assert got.dtype == np.int64 and got[1, 1] == 65536 * 128 * 128
+
+
 def test_w8a8_epilogue_rounding_order():
     rng = np.random.default_rng(12)
     acc = rng.integers(-2**24, 2**24, (4, 5))
