@@ -107,14 +107,17 @@ int64_t tile256_whole(int64_t tiles, int cus) {
 }
 
 // K pieces per tile of the 256-column kernel, variant 1 only: an explicit splits >= 2, or (splits
-// 0) enough pieces to give every CU one when the tiles alone fill fewer than half of them, each
+// 0) enough pieces to give every CU one when the tiles alone fill at most a third of them, each
 // piece at least kMinPieceStages stages of 64 K long (shorter ones spend more on the pipeline's
-// fill and the partial round trip than they gain).
+// fill and the partial round trip than they gain). Between a third and a half the K pieces do not
+// pay for their partials (MI355X, M = 512, K = 3072, weights from HBM: N = 9216, 72 tiles, 3
+// pieces 55.2 vs 60.5 us whole; N = 12288, 96 tiles, 2 pieces 63.1 vs 61.6 us whole), and those
+// plans keep whole tiles and 128-row halves.
 constexpr int kMinPieceStages = 4;
 int tile256_pieces(int tiles, int stages, int splits, int cfg, int cus) {
   if (cfg != kCfgTile256Auto || splits == 1) return 1;
   if (splits >= 2) return std::min(splits, stages);
-  if (2 * tiles > cus) return 1;
+  if (3 * tiles > cus) return 1;
   return std::max(1, std::min(cus / tiles, stages / kMinPieceStages));
 }
 
