@@ -428,10 +428,45 @@ def bench_c4(args):
                     "hbm_frac": round(nbytes / us / 1e3 / PEAK_HBM_GBS, 4)})
         del graph, ws, y
         torch.cuda.empty_cache()
+    # the single-kernel read floor: the same weight + scale bytes read once per call by
+    # qlinear_stream_read (no arithmetic), 12 buffers rotated through 48 graph-captured calls
+    floors = {}
+    for K, N in sorted({(K, N) for _, K, N in shapes}):
+        nb = N * K // 2 + N * (K // 32) * 4
+        bufs = [torch.empty(nb, dtype=torch.uint8, device="cuda").fill_(i + 1) for i in range(12)]
+        out = torch.empty(torch.cuda.get_device_properties(0).multi_processor_count, dtype=torch.int32, device="cuda")
+        with torch.cuda.stream(side):
+            for bb in bufs:
+                _lib.stream_read(bb, out)
+        side.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph, stream=side):
+            for i in range(48):
+                _lib.stream_read(bufs[i % 12], out)
+        graph.replay()
+        torch.cuda.synchronize()
+        times = []
+        for _ in range(5):
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            graph.replay()
+            e1.record()
+            torch.cuda.synchronize()
+            times.append(e0.elapsed_time(e1) * 1e3 / 48)
+        fus = statistics.median(times)
+        floors[(K, N)] = {"bytes": nb, "us_per_call": round(fus, 2), "GB_s": round(nb / fus / 1e3, 1),
+                          "hbm_frac": round(nb / fus / 1e3 / PEAK_HBM_GBS, 4)}
+        del graph, bufs
+        torch.cuda.empty_cache()
+    for r in res:
+        f = floors[(r["K"], r["N"])]
+        r["read_floor_us"] = f["us_per_call"]
+        r["frac_of_read_floor"] = round(f["us_per_call"] / r["us_per_call"], 4)
     print(json.dumps({"metric": "W4A16 skinny-M GB/s vs 8 TB/s HBM (C4)", "unit": "GB/s", "n_gpus": 1,
                       "dtype": "int4 weights, bf16 activations", "data": "synthetic",
                       "timing": "HIP graph of 48 calls over 12 weight copies, replayed back to back",
-                      "results": res}), flush=True)
+                      "results": res,
+                      "read_floor": {f"K={k} N={n}": v for (k, n), v in floors.items()}}), flush=True)
 
 
 def bench_c1(args):

@@ -50,6 +50,7 @@ SIGNATURES = {
     "qlinear_w4a16_gemm": (_c_int, [_c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
                                     _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_int, _c_int, _c_vp, _c_size_t, _c_vp]),
     "qlinear_w4a16_scales_kn": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
+    "qlinear_stream_read": (_c_int, [_c_vp, _c_i64, _c_vp, _c_vp]),
     "qlinear_w4a16_col_scales": (_c_int, [_c_vp, _c_vp, _c_i64, _c_i64, _c_vp]),
     "qlinear_w4a16_out_bound": (_c_int, [_c_vp, _c_vp, _c_vp, _c_int, _c_i64, _c_i64, _c_vp, _c_vp]),
     "qlinear_w4a16_gemm_noalloc": (_c_int, [_c_int, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp,
@@ -182,6 +183,21 @@ def w4a16_col_scales(w_scale: torch.Tensor) -> torch.Tensor:
         rc = lib.qlinear_w4a16_col_scales(w_scale.data_ptr(), cs.data_ptr(), N, G * 32, _stream_ptr(w_scale.device))
     _check(rc, "w4a16_col_scales")
     return cs
+
+
+def stream_read(buf: torch.Tensor, out: torch.Tensor | None = None) -> torch.Tensor:
+    """One read of buf's bytes (qlinear_stream_read, the single-kernel HBM read floor); returns the
+    per-workgroup xor words (uint32 as int32, one per CU)."""
+    lib = load_library()
+    buf = _dev_tensor(buf, "buf")
+    nbytes = buf.numel() * buf.element_size()
+    cus = torch.cuda.get_device_properties(buf.device).multi_processor_count
+    if out is None:
+        out = torch.empty((cus,), dtype=torch.int32, device=buf.device)
+    with torch.cuda.device(buf.device):
+        rc = lib.qlinear_stream_read(buf.data_ptr(), nbytes - nbytes % 16, out.data_ptr(), _stream_ptr(buf.device))
+    _check(rc, "stream_read")
+    return out
 
 
 def w4a16_scales_kn(w_scale: torch.Tensor) -> torch.Tensor:

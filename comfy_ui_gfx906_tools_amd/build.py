@@ -23,7 +23,7 @@ LIB_NAME = "libqlinear.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
 ARCH = "gfx950"
 
-SOURCES = ["w4a16_gemm.hip", "w4a16_tile256.hip", "w4a16_gemv.hip", "w4a16_skinny.hip", "w8a8_gemm.hip", "w8a8_tile256.hip", "quant.hip", "dit_fused.hip", "w4a4_gemm.hip", "rotate.hip", "capi.cpp"]
+SOURCES = ["w4a16_gemm.hip", "w4a16_tile256.hip", "w4a16_gemv.hip", "w4a16_skinny.hip", "w8a8_gemm.hip", "w8a8_tile256.hip", "quant.hip", "dit_fused.hip", "w4a4_gemm.hip", "rotate.hip", "stream_read.hip", "capi.cpp"]
 
 COMMON_FLAGS = [
     "-O3",

@@ -882,6 +882,18 @@ int qlinear_qk_norm_rope(int dtype, const void* qkv, const void* q_norm, const v
   return ok();
 }
 
+int qlinear_stream_read(const void* buf, int64_t bytes, uint32_t* out, void* stream) {
+  if (bytes < 16 || bytes % 16 != 0) return fail(QL_ERR_SHAPE, "bytes must be a positive multiple of 16, got %lld",
+                                                 (long long)bytes);
+  if (!buf || !out) return fail(QL_ERR_ARG, "null buf / out pointer");
+  if (!aligned16(buf)) return fail(QL_ERR_ALIGN, "buf must be 16-byte aligned");
+  int cus = 0;
+  if (int rc = device_cus(-1, &cus)) return rc;
+  const hipError_t e = stream_read_launch(buf, bytes, out, cus, (hipStream_t)stream);
+  if (e != hipSuccess) return fail(QL_ERR_LAUNCH, "stream_read launch failed: %s", hipGetErrorString(e));
+  return ok();
+}
+
 int qlinear_gated_residual(int dtype, void* out, const void* x, const void* gate, const void* y, int64_t M, int64_t K,
                            void* stream) {
   if (dtype != QL_F32 && dtype != QL_F16 && dtype != QL_BF16)

@@ -86,6 +86,8 @@ hipError_t w4a16_reduce_launch(const W4A16Params& p, int BM, int BN, int group_m
 // col_scale[n] = 2^e_n with 8 max_g |w_scale[n, g]| * 2^-e_n in [2^14, 2^15), e_n clamped to
 // [-126, 126]; 1 for a column whose scales are all zero or not finite (w4a16_gemm.hip).
 // w_scale [N, groups] -> w_scale_kn [groups, N] (group-major copy read by the tile kernels)
+// one read of `bytes` bytes (a multiple of 16) by `workgroups` workgroups; xor words to out[workgroups]
+hipError_t stream_read_launch(const void* buf, int64_t bytes, uint32_t* out, int workgroups, hipStream_t stream);
 hipError_t scales_kn_launch(const float* w_scale, float* w_scale_kn, int64_t N, int64_t groups, hipStream_t stream);
 hipError_t col_scales_launch(const float* w_scale, float* col_scale, int64_t N, int64_t groups, hipStream_t stream);
 // bound[0] = max_n sum_k |q_nk s_n,k/32| (1 + 2^-10), bound[1] = max_n |bias_n| (0 without bias);

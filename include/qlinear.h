@@ -343,6 +343,12 @@ int qlinear_heads_to_f16(int dtype, const void* o, int64_t H, int64_t L_all, int
                          int64_t l_offset, int64_t rows, const void* extra, int64_t E, void* x16,
                          float* row_scale, void* stream);
 
+/* Measurement: one read of `bytes` bytes of buf (a multiple of 16, 16-byte aligned) by one
+ * workgroup per CU with 16-byte loads, folded to one xor word per workgroup into out (as many
+ * uint32 as the device has CUs). The single-kernel HBM read floor the skinny-M W4A16 kernels
+ * (which read their weights once per call) are measured against. No counterpart in the reference. */
+int qlinear_stream_read(const void* buf, int64_t bytes, uint32_t* out, void* stream);
+
 /* Gated residual: out[m, k] = x[m, k] + gate[k] * y[m, k]; out may be x (in place) but must
  * not overlap it otherwise; out, x, gate, y of one dtype (fp32/fp16/bf16), K % 8 == 0, 16-byte
  * aligned. */
