@@ -63,6 +63,8 @@ SIGNATURES = {
     "qlinear_w8a8_gemm": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64, _c_i64, _c_vp]),
     "qlinear_adaln_modulate_f16": (_c_int, [_c_int, _c_vp, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64,
                                             ctypes.c_float, _c_vp]),
+    "qlinear_heads_gather": (_c_int, [_c_int, _c_int, _c_vp, _c_i64, _c_i64, _c_i64, _c_i64, _c_i64, _c_vp, _c_i64,
+                                      _c_vp, _c_vp, _c_vp]),
     "qlinear_adaln_modulate": (_c_int, [_c_int, _c_int, _c_vp, _c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64,
                                         ctypes.c_float, _c_vp]),
     "qlinear_qk_norm_rope": (_c_int, [_c_int, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_vp, _c_i64, _c_i64,
@@ -717,7 +719,7 @@ def adaln_modulate_f16(x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor
     return x16, rs
 
 
-ADALN_F16_ROWSCALED, ADALN_PLAIN, ADALN_I8_PER_TOKEN = 0, 1, 2
+OPERAND_F16_ROWSCALED, OPERAND_PLAIN, OPERAND_I8_PER_TOKEN = 0, 1, 2
 
 
 def adaln_modulate(x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor, out: str = "f16",
@@ -727,7 +729,7 @@ def adaln_modulate(x: torch.Tensor, shift: torch.Tensor, scale: torch.Tensor, ou
     x's dtype [M, K]; "i8" -> (q int8 [M, K], scale fp32 [M]), the W8A8 GEMM's per-token operand
     (the plain output quantized by quantize_int8_per_token's rule, in the same pass)."""
     lib = load_library()
-    kinds = {"f16": ADALN_F16_ROWSCALED, "plain": ADALN_PLAIN, "i8": ADALN_I8_PER_TOKEN}
+    kinds = {"f16": OPERAND_F16_ROWSCALED, "plain": OPERAND_PLAIN, "i8": OPERAND_I8_PER_TOKEN}
     if out not in kinds:
         raise RuntimeError(f"out must be one of {sorted(kinds)}, got {out!r}")
     x = _dev_tensor(x, "x")
@@ -836,3 +838,34 @@ def heads_to_f16(o: torch.Tensor, l_offset: int = 0, rows: int | None = None,
                                       rs.data_ptr(), _stream_ptr(o.device))
     _check(rc, "heads_to_f16")
     return x16, rs
+
+
+def heads_gather(o: torch.Tensor, l_offset: int = 0, rows: int | None = None, extra: torch.Tensor | None = None,
+                 out: str = "f16"):
+    """heads_to_f16's gathered rows written as `out`: "f16" -> (x16, row_scale) as heads_to_f16;
+    "plain" -> the rows in o's dtype [rows, H * 128 + E]; "i8" -> (q int8, scale fp32 [rows]), the
+    W8A8 GEMM's per-token operand (quantize_int8_per_token's rule, in the same pass)."""
+    lib = load_library()
+    kinds = {"f16": OPERAND_F16_ROWSCALED, "plain": OPERAND_PLAIN, "i8": OPERAND_I8_PER_TOKEN}
+    if out not in kinds:
+        raise RuntimeError(f"out must be one of {sorted(kinds)}, got {out!r}")
+    o = _dev_tensor(o, "o")
+    if o.dim() != 3 or o.shape[2] != 128 or o.dtype not in (torch.bfloat16, torch.float16):
+        raise RuntimeError(f"o must be a bfloat16/float16 [H, L, 128] tensor, got {o.dtype} {tuple(o.shape)}")
+    H, L = o.shape[0], o.shape[1]
+    rows = L - l_offset if rows is None else rows
+    E = 0
+    if extra is not None:
+        extra = _dev_tensor(extra, "extra")
+        if extra.dtype != o.dtype or extra.dim() != 2 or extra.shape[0] != rows:
+            raise RuntimeError(f"extra must be a {o.dtype} [{rows}, E] tensor, got {extra.dtype} {tuple(extra.shape)}")
+        E = extra.shape[1]
+    odt = {"f16": torch.float16, "plain": o.dtype, "i8": torch.int8}[out]
+    y = torch.empty((rows, H * 128 + E), dtype=odt, device=o.device)
+    rs = torch.empty((rows,), dtype=torch.float32, device=o.device) if out != "plain" else None
+    with torch.cuda.device(o.device):
+        rc = lib.qlinear_heads_gather(kinds[out], _DTYPE_CODE[o.dtype], o.data_ptr(), H, L, 128, l_offset, rows,
+                                      extra.data_ptr() if extra is not None else None, E, y.data_ptr(),
+                                      rs.data_ptr() if rs is not None else None, _stream_ptr(o.device))
+    _check(rc, "heads_gather")
+    return y if out == "plain" else (y, rs)

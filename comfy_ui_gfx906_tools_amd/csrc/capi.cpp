@@ -826,8 +826,8 @@ int qlinear_w8a8_gemm(int out_dtype, const int8_t* xq, const float* x_scale, con
 int qlinear_adaln_modulate(int out_kind, int x_dtype, const void* x, int mod_dtype, const void* shift,
                            const void* scale, void* out, float* row_scale, int64_t M, int64_t K, float eps,
                            void* stream) {
-  if (out_kind != QL_ADALN_F16_ROWSCALED && out_kind != QL_ADALN_PLAIN && out_kind != QL_ADALN_I8_PER_TOKEN)
-    return fail(QL_ERR_ARG, "out_kind must be QL_ADALN_F16_ROWSCALED, QL_ADALN_PLAIN or QL_ADALN_I8_PER_TOKEN, got %d",
+  if (out_kind != QL_OPERAND_F16_ROWSCALED && out_kind != QL_OPERAND_PLAIN && out_kind != QL_OPERAND_I8_PER_TOKEN)
+    return fail(QL_ERR_ARG, "out_kind must be QL_OPERAND_F16_ROWSCALED, QL_OPERAND_PLAIN or QL_OPERAND_I8_PER_TOKEN, got %d",
                 out_kind);
   if (x_dtype != QL_F32 && x_dtype != QL_F16 && x_dtype != QL_BF16)
     return fail(QL_ERR_DTYPE, "x dtype %s (%d) unsupported, expected float32/float16/bfloat16", dtype_name(x_dtype),
@@ -840,12 +840,12 @@ int qlinear_adaln_modulate(int out_kind, int x_dtype, const void* x, int mod_dty
                 (long long)K);
   if (!(eps >= 0.0f)) return fail(QL_ERR_ARG, "eps must be >= 0, got %g", (double)eps);
   if (M == 0) return ok();
-  if (!x || !shift || !scale || !out || (out_kind != QL_ADALN_PLAIN && !row_scale))
+  if (!x || !shift || !scale || !out || (out_kind != QL_OPERAND_PLAIN && !row_scale))
     return fail(QL_ERR_ARG, "null x / shift / scale / out / row_scale pointer");
   if (!aligned16(x) || !aligned16(shift) || !aligned16(scale) ||
-      (out_kind == QL_ADALN_I8_PER_TOKEN ? ((uintptr_t)out & 7) != 0 : !aligned16(out)))
+      (out_kind == QL_OPERAND_I8_PER_TOKEN ? ((uintptr_t)out & 7) != 0 : !aligned16(out)))
     return fail(QL_ERR_ALIGN, "x, shift, scale and out must be 16-byte aligned (int8 out: 8-byte)");
-  const int kind = out_kind == QL_ADALN_PLAIN ? kAdalnPlain : out_kind == QL_ADALN_I8_PER_TOKEN ? kAdalnI8 : kAdalnF16;
+  const int kind = out_kind == QL_OPERAND_PLAIN ? kOperandPlain : out_kind == QL_OPERAND_I8_PER_TOKEN ? kOperandI8 : kOperandF16;
   const hipError_t e = adaln_launch(kind, x_dtype, mod_dtype, x, shift, scale, out, row_scale, M, K, eps,
                                     (hipStream_t)stream);
   if (e != hipSuccess) return fail(QL_ERR_LAUNCH, "adaln_modulate launch failed: %s", hipGetErrorString(e));
@@ -854,7 +854,7 @@ int qlinear_adaln_modulate(int out_kind, int x_dtype, const void* x, int mod_dty
 
 int qlinear_adaln_modulate_f16(int x_dtype, const void* x, int mod_dtype, const void* shift, const void* scale,
                                void* x16, float* row_scale, int64_t M, int64_t K, float eps, void* stream) {
-  return qlinear_adaln_modulate(QL_ADALN_F16_ROWSCALED, x_dtype, x, mod_dtype, shift, scale, x16, row_scale, M, K, eps,
+  return qlinear_adaln_modulate(QL_OPERAND_F16_ROWSCALED, x_dtype, x, mod_dtype, shift, scale, x16, row_scale, M, K, eps,
                                 stream);
 }
 
@@ -999,8 +999,11 @@ int qlinear_rotate_rows_to_f16(int x_dtype, const void* x, const float* signs, i
   return ok();
 }
 
-int qlinear_heads_to_f16(int dtype, const void* o, int64_t H, int64_t L_all, int64_t D, int64_t l_offset, int64_t rows,
-                         const void* extra, int64_t E, void* x16, float* row_scale, void* stream) {
+int qlinear_heads_gather(int out_kind, int dtype, const void* o, int64_t H, int64_t L_all, int64_t D, int64_t l_offset,
+                         int64_t rows, const void* extra, int64_t E, void* out, float* row_scale, void* stream) {
+  if (out_kind != QL_OPERAND_F16_ROWSCALED && out_kind != QL_OPERAND_PLAIN && out_kind != QL_OPERAND_I8_PER_TOKEN)
+    return fail(QL_ERR_ARG, "out_kind must be QL_OPERAND_F16_ROWSCALED, QL_OPERAND_PLAIN or QL_OPERAND_I8_PER_TOKEN, got %d",
+                out_kind);
   if (dtype != QL_F16 && dtype != QL_BF16)
     return fail(QL_ERR_DTYPE, "dtype %s (%d) unsupported, expected float16/bfloat16", dtype_name(dtype), dtype);
   if (D != 128) return fail(QL_ERR_SHAPE, "head dim must be 128, got %lld", (long long)D);
@@ -1010,13 +1013,22 @@ int qlinear_heads_to_f16(int dtype, const void* o, int64_t H, int64_t L_all, int
                 "E %% 8 == 0, H * 128 + E <= 16384; got H=%lld L_all=%lld l_offset=%lld rows=%lld E=%lld", (long long)H,
                 (long long)L_all, (long long)l_offset, (long long)rows, (long long)E);
   if (rows == 0) return ok();
-  if (!o || !x16 || !row_scale || (E > 0 && !extra)) return fail(QL_ERR_ARG, "null o / extra / x16 / row_scale pointer");
-  if (!aligned16(o) || !aligned16(x16) || (E > 0 && !aligned16(extra)))
-    return fail(QL_ERR_ALIGN, "o, extra and x16 must be 16-byte aligned");
-  const hipError_t e = heads_to_f16_launch(dtype, o, H, L_all, l_offset, rows, E > 0 ? extra : nullptr, E, x16,
+  if (!o || !out || (out_kind != QL_OPERAND_PLAIN && !row_scale) || (E > 0 && !extra))
+    return fail(QL_ERR_ARG, "null o / extra / out / row_scale pointer");
+  if (!aligned16(o) || (E > 0 && !aligned16(extra)) ||
+      (out_kind == QL_OPERAND_I8_PER_TOKEN ? ((uintptr_t)out & 7) != 0 : !aligned16(out)))
+    return fail(QL_ERR_ALIGN, "o, extra and out must be 16-byte aligned (int8 out: 8-byte)");
+  const int kind = out_kind == QL_OPERAND_PLAIN ? kOperandPlain : out_kind == QL_OPERAND_I8_PER_TOKEN ? kOperandI8 : kOperandF16;
+  const hipError_t e = heads_gather_launch(kind, dtype, o, H, L_all, l_offset, rows, E > 0 ? extra : nullptr, E, out,
                                            row_scale, (hipStream_t)stream);
-  if (e != hipSuccess) return fail(QL_ERR_LAUNCH, "heads_to_f16 launch failed: %s", hipGetErrorString(e));
+  if (e != hipSuccess) return fail(QL_ERR_LAUNCH, "heads_gather launch failed: %s", hipGetErrorString(e));
   return ok();
+}
+
+int qlinear_heads_to_f16(int dtype, const void* o, int64_t H, int64_t L_all, int64_t D, int64_t l_offset, int64_t rows,
+                         const void* extra, int64_t E, void* x16, float* row_scale, void* stream) {
+  return qlinear_heads_gather(QL_OPERAND_F16_ROWSCALED, dtype, o, H, L_all, D, l_offset, rows, extra, E, x16, row_scale,
+                              stream);
 }
 
 int qlinear_quantize_int8_block32(int x_dtype, const void* x, int8_t* q, float* scale, int64_t rows, int64_t K,

@@ -90,8 +90,8 @@ __device__ __forceinline__ float block_max(float v, float* red) {
 }
 
 // One 256-thread block per row; thread t holds elements 8t + 2048 r (r < R) in registers, so the
-// row is read from HBM once. K % 8 == 0, K <= 2048 R. OUT: kAdalnF16 the row-scaled fp16 operand
-// of the W4A16 GEMM, kAdalnPlain the row in x's dtype, kAdalnI8 the per-token int8 operand of the
+// row is read from HBM once. K % 8 == 0, K <= 2048 R. OUT: kOperandF16 the row-scaled fp16 operand
+// of the W4A16 GEMM, kOperandPlain the row in x's dtype, kOperandI8 the per-token int8 operand of the
 // W8A8 GEMM: the row rounded to x's dtype, then quantized by qlinear_quantize_int8_per_token's
 // rule (s = fl(max(amax, 1e-8) * fl(1/127)), q = clamp(rint(v / s), -127, 127), IEEE division),
 // row_scale[m] = s.
@@ -137,12 +137,12 @@ __global__ __launch_bounds__(256) void adaln_to_f16_kernel(const void* __restric
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         v[r][e] = (v[r][e] - mean) * rstd * (1.0f + sc[e]) + sh[e];
-        if constexpr (OUT == kAdalnI8) v[r][e] = round_to(XDT, v[r][e]);
+        if constexpr (OUT == kOperandI8) v[r][e] = round_to(XDT, v[r][e]);
         amax = fmaxf(amax, fabsf(v[r][e]));
       }
     }
   }
-  if constexpr (OUT == kAdalnPlain) {
+  if constexpr (OUT == kOperandPlain) {
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int k = threadIdx.x * 8 + r * 2048;
@@ -151,7 +151,7 @@ __global__ __launch_bounds__(256) void adaln_to_f16_kernel(const void* __restric
     return;
   }
   amax = block_max(amax, red[2]);
-  if constexpr (OUT == kAdalnI8) {
+  if constexpr (OUT == kOperandI8) {
     const float s = __fmul_rn(fmaxf(amax, 1e-8f), 1.0f / 127.0f);
     if (threadIdx.x == 0) row_scale[blockIdx.x] = s;
 #pragma unroll
@@ -243,9 +243,12 @@ __global__ __launch_bounds__(256) void gated_residual_kernel(void* out, const vo
 
 // One 256-thread block per output row l; thread t holds row elements 8t + 2048 r (r < R): element
 // p < H * 128 is o[p / 128, l0 + l, p % 128], element p >= H * 128 is extra[l, p - H * 128].
-template <int DT, int R>
+// OUT as for adaln_to_f16_kernel: the row-scaled fp16 operand, the gathered row itself (DT), or
+// the per-token int8 operand (the gathered values are the inputs themselves, so no rounding comes
+// first).
+template <int DT, int R, int OUT>
 __global__ __launch_bounds__(256) void heads_to_f16_kernel(const void* __restrict__ o, const void* __restrict__ extra,
-                                                           _Float16* __restrict__ x16, float* __restrict__ row_scale,
+                                                           void* __restrict__ out, float* __restrict__ row_scale,
                                                            int H, int L_all, int l0, int E) {
   constexpr int D = 128;
   __shared__ float red[4];
@@ -265,7 +268,34 @@ __global__ __launch_bounds__(256) void heads_to_f16_kernel(const void* __restric
       for (int e = 0; e < 8; ++e) amax = fmaxf(amax, fabsf(v[r][e]));
     }
   }
+  if constexpr (OUT == kOperandPlain) {
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int p = threadIdx.x * 8 + r * 2048;
+      if (p < Kt) store8<DT>(out, (size_t)l * Kt + p, v[r]);
+    }
+    return;
+  }
   amax = block_max(amax, red);
+  if constexpr (OUT == kOperandI8) {  // the rule of qlinear_quantize_int8_per_token
+    const float s = __fmul_rn(fmaxf(amax, 1e-8f), 1.0f / 127.0f);
+    if (threadIdx.x == 0) row_scale[l] = s;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int p = threadIdx.x * 8 + r * 2048;
+      if (p < Kt) {
+        uint32_t w[2] = {0u, 0u};
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int c = (int)fminf(fmaxf(rintf(__fdiv_rn(v[r][e], s)), -127.0f), 127.0f);
+          w[e >> 2] |= ((uint32_t)c & 0xFFu) << (8 * (e & 3));
+        }
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        *(u32x2*)((int8_t*)out + (size_t)l * Kt + p) = u32x2{w[0], w[1]};
+      }
+    }
+    return;
+  }
   int ex = 0;
   if (amax > 0.0f && amax <= 3.0e38f) {
     int E2;
@@ -280,7 +310,7 @@ __global__ __launch_bounds__(256) void heads_to_f16_kernel(const void* __restric
       float q[8];
 #pragma unroll
       for (int e = 0; e < 8; ++e) q[e] = ldexpf(v[r][e], -ex);
-      store8<kF16>(x16, (size_t)l * Kt + p, q);
+      store8<kF16>(out, (size_t)l * Kt + p, q);
     }
   }
 }
@@ -329,10 +359,10 @@ hipError_t adaln_launch_o(int x_dtype, int mod_dtype, const void* x, const void*
 hipError_t adaln_launch(int out_kind, int x_dtype, int mod_dtype, const void* x, const void* shift, const void* scale,
                         void* out, float* row_scale, int64_t M, int64_t K, float eps, hipStream_t stream) {
   switch (out_kind) {
-    case kAdalnF16: return adaln_launch_o<kAdalnF16>(x_dtype, mod_dtype, x, shift, scale, out, row_scale, M, K, eps, stream);
-    case kAdalnPlain:
-      return adaln_launch_o<kAdalnPlain>(x_dtype, mod_dtype, x, shift, scale, out, row_scale, M, K, eps, stream);
-    case kAdalnI8: return adaln_launch_o<kAdalnI8>(x_dtype, mod_dtype, x, shift, scale, out, row_scale, M, K, eps, stream);
+    case kOperandF16: return adaln_launch_o<kOperandF16>(x_dtype, mod_dtype, x, shift, scale, out, row_scale, M, K, eps, stream);
+    case kOperandPlain:
+      return adaln_launch_o<kOperandPlain>(x_dtype, mod_dtype, x, shift, scale, out, row_scale, M, K, eps, stream);
+    case kOperandI8: return adaln_launch_o<kOperandI8>(x_dtype, mod_dtype, x, shift, scale, out, row_scale, M, K, eps, stream);
     default: return hipErrorInvalidValue;
   }
 }
@@ -351,14 +381,14 @@ hipError_t qk_norm_rope_launch(int dtype, const void* qkv, const void* q_norm, c
   return hipGetLastError();
 }
 
-template <int DT>
+template <int DT, int OUT>
 static hipError_t heads_launch_r(const void* o, const void* extra, void* x16, float* rs, int64_t H, int64_t L_all,
                                  int64_t l0, int64_t rows, int64_t E, hipStream_t st) {
   const int64_t Kt = H * 128 + E;
   const dim3 grid((unsigned)rows), block(256);
-#define QL_HEADS(R)                                                                                         \
-  hipLaunchKernelGGL((heads_to_f16_kernel<DT, R>), grid, block, 0, st, o, extra, (_Float16*)x16, rs, (int)H, \
-                     (int)L_all, (int)l0, (int)E)
+#define QL_HEADS(R)                                                                                       \
+  hipLaunchKernelGGL((heads_to_f16_kernel<DT, R, OUT>), grid, block, 0, st, o, extra, x16, rs, (int)H, (int)L_all, \
+                     (int)l0, (int)E)
   if (Kt <= 2048)
     QL_HEADS(1);
   else if (Kt <= 4096)
@@ -371,10 +401,23 @@ static hipError_t heads_launch_r(const void* o, const void* extra, void* x16, fl
   return hipGetLastError();
 }
 
-hipError_t heads_to_f16_launch(int dtype, const void* o, int64_t H, int64_t L_all, int64_t l0, int64_t rows,
-                               const void* extra, int64_t E, void* x16, float* row_scale, hipStream_t stream) {
-  return dtype == kBF16 ? heads_launch_r<kBF16>(o, extra, x16, row_scale, H, L_all, l0, rows, E, stream)
-                        : heads_launch_r<kF16>(o, extra, x16, row_scale, H, L_all, l0, rows, E, stream);
+template <int OUT>
+static hipError_t heads_launch_o(int dtype, const void* o, int64_t H, int64_t L_all, int64_t l0, int64_t rows,
+                                 const void* extra, int64_t E, void* out, float* row_scale, hipStream_t stream) {
+  return dtype == kBF16 ? heads_launch_r<kBF16, OUT>(o, extra, out, row_scale, H, L_all, l0, rows, E, stream)
+                        : heads_launch_r<kF16, OUT>(o, extra, out, row_scale, H, L_all, l0, rows, E, stream);
+}
+
+hipError_t heads_gather_launch(int out_kind, int dtype, const void* o, int64_t H, int64_t L_all, int64_t l0,
+                               int64_t rows, const void* extra, int64_t E, void* out, float* row_scale,
+                               hipStream_t stream) {
+  switch (out_kind) {
+    case kOperandF16: return heads_launch_o<kOperandF16>(dtype, o, H, L_all, l0, rows, extra, E, out, row_scale, stream);
+    case kOperandPlain:
+      return heads_launch_o<kOperandPlain>(dtype, o, H, L_all, l0, rows, extra, E, out, row_scale, stream);
+    case kOperandI8: return heads_launch_o<kOperandI8>(dtype, o, H, L_all, l0, rows, extra, E, out, row_scale, stream);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 hipError_t gated_residual_launch(int dtype, void* out, const void* x, const void* gate, const void* y, int64_t M,

@@ -152,9 +152,9 @@ hipError_t rotate_rows_to_f16_launch(int x_dtype, int group, const void* x, cons
 
 // Fused DiT block glue (dit_fused.hip). K % 8 == 0 and K <= 16384 for the LayerNorm kernel;
 // head dim 128 for the q/k kernel; K % 8 == 0 for the residual.
-// adaLN of rows of x into: kAdalnF16 the row-scaled fp16 W4A16 operand (+ row_scale), kAdalnPlain
-// x's dtype, kAdalnI8 the per-token int8 W8A8 operand (+ its scales in row_scale)
-constexpr int kAdalnF16 = 0, kAdalnPlain = 1, kAdalnI8 = 2;
+// adaLN of rows of x into: kOperandF16 the row-scaled fp16 W4A16 operand (+ row_scale), kOperandPlain
+// x's dtype, kOperandI8 the per-token int8 W8A8 operand (+ its scales in row_scale)
+constexpr int kOperandF16 = 0, kOperandPlain = 1, kOperandI8 = 2;
 hipError_t adaln_launch(int out_kind, int x_dtype, int mod_dtype, const void* x, const void* shift, const void* scale,
                         void* out, float* row_scale, int64_t M, int64_t K, float eps, hipStream_t stream);
 hipError_t qk_norm_rope_launch(int dtype, const void* qkv, const void* q_norm, const void* k_norm, const float* cosv,
@@ -162,7 +162,8 @@ hipError_t qk_norm_rope_launch(int dtype, const void* qkv, const void* q_norm, c
                                int64_t l0, float eps, hipStream_t stream);
 hipError_t gated_residual_launch(int dtype, void* out, const void* x, const void* gate, const void* y, int64_t M,
                                  int64_t K, hipStream_t stream);
-hipError_t heads_to_f16_launch(int dtype, const void* o, int64_t H, int64_t L_all, int64_t l0, int64_t rows,
-                               const void* extra, int64_t E, void* x16, float* row_scale, hipStream_t stream);
+hipError_t heads_gather_launch(int out_kind, int dtype, const void* o, int64_t H, int64_t L_all, int64_t l0,
+                               int64_t rows, const void* extra, int64_t E, void* out, float* row_scale,
+                               hipStream_t stream);
 
 }  // namespace qlinear

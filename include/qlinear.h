@@ -307,18 +307,18 @@ int qlinear_adaln_modulate_f16(int x_dtype, const void* x, int mod_dtype, const 
                                int64_t K, float eps, void* stream);
 
 /* The same adaLN row y written as out_kind says:
- *   QL_ADALN_F16_ROWSCALED  as qlinear_adaln_modulate_f16 (out = x16 fp16, row_scale = 2^e_m);
- *   QL_ADALN_PLAIN          y rounded to x's dtype, out [M, K] of that dtype (row_scale unused);
- *   QL_ADALN_I8_PER_TOKEN   the W8A8 GEMM's operand: y rounded to x's dtype, then quantized as
+ *   QL_OPERAND_F16_ROWSCALED  as qlinear_adaln_modulate_f16 (out = x16 fp16, row_scale = 2^e_m);
+ *   QL_OPERAND_PLAIN          y rounded to x's dtype, out [M, K] of that dtype (row_scale unused);
+ *   QL_OPERAND_I8_PER_TOKEN   the W8A8 GEMM's operand: y rounded to x's dtype, then quantized as
  *                           qlinear_quantize_int8_per_token quantizes it (out int8 [M, K],
  *                           row_scale[m] = the token's scale) -- the PLAIN output followed by
  *                           that quantizer, bit for bit, without the round trip of the bf16 row
  *                           through HBM (the reference quantizes in a launch of its own,
  *                           ops.py:181, csrc/int8_gemm.hip:215-246).
  * out 16-byte aligned (8-byte for int8). */
-#define QL_ADALN_F16_ROWSCALED 0
-#define QL_ADALN_PLAIN 1
-#define QL_ADALN_I8_PER_TOKEN 2
+#define QL_OPERAND_F16_ROWSCALED 0
+#define QL_OPERAND_PLAIN 1
+#define QL_OPERAND_I8_PER_TOKEN 2
 int qlinear_adaln_modulate(int out_kind, int x_dtype, const void* x, int mod_dtype,
                            const void* shift, const void* scale, void* out, float* row_scale,
                            int64_t M, int64_t K, float eps, void* stream);
@@ -342,6 +342,16 @@ int qlinear_qk_norm_rope(int dtype, const void* qkv, const void* q_norm, const v
 int qlinear_heads_to_f16(int dtype, const void* o, int64_t H, int64_t L_all, int64_t D,
                          int64_t l_offset, int64_t rows, const void* extra, int64_t E, void* x16,
                          float* row_scale, void* stream);
+
+/* The same gathered row written as out_kind says (the QL_OPERAND_* kinds of
+ * qlinear_adaln_modulate): QL_OPERAND_F16_ROWSCALED as qlinear_heads_to_f16; QL_OPERAND_PLAIN the
+ * row in `dtype` ([rows, H * D + E], row_scale unused); QL_OPERAND_I8_PER_TOKEN the W8A8 operand,
+ * the row quantized as qlinear_quantize_int8_per_token quantizes it (int8 out, row_scale[l] = the
+ * token's scale) -- the producer of a W8A8 proj / linear2 writing its operand directly. out 16-byte
+ * aligned (8-byte for int8). */
+int qlinear_heads_gather(int out_kind, int dtype, const void* o, int64_t H, int64_t L_all,
+                         int64_t D, int64_t l_offset, int64_t rows, const void* extra, int64_t E,
+                         void* out, float* row_scale, void* stream);
 
 /* Measurement: one read of `bytes` bytes of buf (a multiple of 16, 16-byte aligned) by one
  * workgroup per CU with 16-byte loads, folded to one xor word per workgroup into out (as many

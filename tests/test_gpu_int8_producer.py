@@ -1,6 +1,6 @@
-"""The per-token int8 quantize fused into its producer (qlinear_adaln_modulate with
-QL_ADALN_I8_PER_TOKEN): the adaLN row that feeds a W8A8 linear is written straight as the W8A8
-GEMM's operand.
+"""The per-token int8 quantize fused into its producers (qlinear_adaln_modulate and
+qlinear_heads_gather with QL_OPERAND_I8_PER_TOKEN): the adaLN row that feeds a W8A8 linear, and the
+attention output gathered for the next linear, are written straight as the W8A8 GEMM's operand.
 
 Pinned bit for bit against the unfused pair on the same GPU -- the plain adaLN output (x's dtype)
 followed by qlinear_quantize_int8_per_token, the reference's per-token int8 rule (csrc/
@@ -77,3 +77,25 @@ def test_adaln_modulate_argument_checks():
     # int8 output needs its scales
     assert lib.qlinear_adaln_modulate(2, 2, x.data_ptr(), 2, sh.data_ptr(), sh.data_ptr(), x.data_ptr(), None, 4, 64,
                                       1e-6, None) != 0
+
+
+@pytest.mark.parametrize("H,L,l0,rows,E,dt", [(24, 700, 100, 512, 0, torch.bfloat16), (24, 300, 0, 300, 256, torch.float16),
+                                             (8, 64, 3, 17, 8, torch.bfloat16)])
+def test_heads_gather_i8_equals_plain_then_quantize(H, L, l0, rows, E, dt):
+    """The attention-output gather: the plain rows equal torch's transpose + concatenation, and the
+    int8 operand equals qlinear_quantize_int8_per_token of them bit for bit."""
+    print(f"heads gather i8 H={H} L={L} l0={l0} rows={rows} E={E} {dt}", flush=True)
+    g = torch.Generator(device="cuda").manual_seed(H + L + E)
+    o = torch.randn(H, L, 128, device="cuda", generator=g).to(dt)
+    extra = torch.randn(rows, E, device="cuda", generator=g).to(dt) if E else None
+    plain = _lib.heads_gather(o, l_offset=l0, rows=rows, extra=extra, out="plain")
+    ref = o[:, l0:l0 + rows].permute(1, 0, 2).reshape(rows, H * 128)
+    if extra is not None:
+        ref = torch.cat([ref, extra], dim=1)
+    assert torch.equal(plain, ref)
+    q, s = _lib.heads_gather(o, l_offset=l0, rows=rows, extra=extra, out="i8")
+    q_ref, s_ref = _lib.quantize_int8_per_token(plain)
+    assert torch.equal(s, s_ref) and torch.equal(q, q_ref)
+    x16, rs = _lib.heads_gather(o, l_offset=l0, rows=rows, extra=extra, out="f16")
+    x16b, rsb = _lib.heads_to_f16(o, l_offset=l0, rows=rows, extra=extra)
+    assert torch.equal(x16, x16b) and torch.equal(rs, rsb)
