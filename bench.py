@@ -506,8 +506,11 @@ def bench_c1(args):
         torch.cuda.synchronize()
         return out, e0.elapsed_time(e1) / args.steps
 
-    csd = _lib.w4a16_col_scales(wsd)  # the fp16 dequant's column factors, kept with the weight
-    y16, ms16 = timed(lambda: _lib.w4a16_gemm(xd, wqd, wsd, None, out_dtype=torch.float16, col_scale=csd))
+    # the fp16 dequant's column factors and the group-major scale copy, both kept with the weight
+    # (as Gfx906Int4Ops.Linear keeps them)
+    csd, knd = _lib.w4a16_col_scales(wsd), _lib.w4a16_scales_kn(wsd)
+    y16, ms16 = timed(lambda: _lib.w4a16_gemm(xd, wqd, wsd, None, out_dtype=torch.float16, col_scale=csd,
+                                              scales_kn=knd))
     y32 = _lib.w4a16_gemm(xd, wqd, wsd, None, out_dtype=torch.float32)
     ref = xd.float() @ dequant_fp32(wqd, wsd).t()
     err = ((y32 - ref).abs().max() / ref.abs().max()).item()
@@ -525,7 +528,7 @@ def bench_c1(args):
     _, ms_rot = timed(lambda: ops.int4_linear(xd, wqd, wsd, None, rotation_group=grp))
     R = ops.get_group_rotation(K, grp, xd.device)
     _, ms_rot_unfused = timed(lambda: _lib.w4a16_gemm(ops.apply_group_rotation(xd.float(), R, grp), wqd, wsd, None,
-                                                      out_dtype=torch.float16, col_scale=csd))
+                                                      out_dtype=torch.float16, col_scale=csd, scales_kn=knd))
     flops = 2.0 * M * N * K
     out = {"metric": "W4A16 GEMM TFLOP/s at the C1 shape (x fp16 [4608, 3072], W [3072, 3072] int4 g32)",
            "value": round(flops / (ms16 * 1e-3) / 1e12, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
