@@ -121,6 +121,31 @@ int tile256_pieces(int tiles, int stages, int splits, int cfg, int cus) {
   return std::max(1, std::min(cus / tiles, stages / kMinPieceStages));
 }
 
+// K pieces of the 4-wave kernel (configurations 0-3) with splits 0: when the last round of tiles
+// fills the CUs badly (under 92%), its tiles are cut into the k pieces that minimize the modelled
+// time ceil(rem k / CUs) / k (+ 1% per piece for the partial round trip); *dp = the tiles that
+// run whole (the full rounds), the rest are cut. Returns 1 when nothing is cut (*dp = tiles).
+int four_wave_pieces(int tiles, int stages, int cus, int* dp) {
+  *dp = tiles;
+  if (stages < 2) return 1;
+  const int waves = (tiles + cus - 1) / cus;
+  if ((double)tiles / ((double)waves * cus) >= 0.92) return 1;
+  const int whole = (tiles / cus) * cus;
+  const int rem = tiles - whole;
+  double best = (double)((rem + cus - 1) / cus);
+  int best_k = 1;
+  for (int k = 2; k <= std::min(stages, 16); ++k) {
+    const double t = (double)(((int64_t)rem * k + cus - 1) / cus) / k + 0.01 * k;
+    if (t < best - 1e-9) {
+      best = t;
+      best_k = k;
+    }
+  }
+  if (best_k == 1 || rem > kMaxCutTiles) return 1;
+  *dp = whole;
+  return best_k;
+}
+
 // 256 x 256 tiles once there are at least a quarter as many as CUs. Measured on MI355X (bf16 x via
 // the fp16 staging, Flux DiT shapes): the 128-row kernel spends 1.6-2.2x the time per flop, so the
 // 256 x 256 kernel wins even with most CUs idle (M=4096 N=3072 K=3072, 192 tiles: 80 vs 128 us;
@@ -179,7 +204,22 @@ int w4a16_cfg_for(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, int 
   // from HBM: K = 4096, N = 10240, M = 64 28.7 vs 27.4 us, M = 128 35.4 vs 35.3 us.)
   if (M <= 64) return 2;
   if (M <= 128) return 1;
-  return (splits < 2 && prefer_tile256(M, N, K, cus)) ? kCfgTile256Auto : 1;
+  if (splits < 2 && prefer_tile256(M, N, K, cus)) return kCfgTile256Auto;
+  // Fewer 256 x 256 tiles than that: the 128-row tiles with K pieces, unless their pieces need
+  // more than one round of workgroups; then the 256 x 256 tiles cut into K pieces (one round)
+  // win. Measured on MI355X, fp16 x, weights from HBM, us 128-row plan vs 256 x 256 pieces: over
+  // one round M=768 K=3072 N=3072 (504 workgroups) 57.6 vs 41.7, M=1024 480 workgroups 57.2 vs
+  // 44.2, M=512 N=6144 53.8 vs 43.3, M=768 and 1024 at K=12288 89.1 vs 76.3 and 107.7 vs 90.9;
+  // one round or less M=512 N=3072 29.8 vs 35.0, K=12288 55.9 vs 57.9, M=640 30.3 vs 39.3,
+  // M=896 37.0 vs 41.6, M=1024 N=2048 31.6 vs 40.0, M=256 K=4096 N=10240 41.9 vs 45.2.
+  if (splits == 0 && K % 64 == 0) {
+    const W4A16Config& c = w4a16_config(1);
+    const int tiles = (int)(((M + c.BM - 1) / c.BM) * ((N + c.BN - 1) / c.BN));
+    int dp = tiles;
+    const int k = four_wave_pieces(tiles, w4a16_steps(1, K), cus, &dp);
+    if (dp + (int64_t)(tiles - dp) * k > cus) return kCfgTile256Auto;
+  }
+  return 1;
 }
 
 W4A16Plan plan_w4a16(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, int flags, int cus) {
@@ -228,26 +268,8 @@ W4A16Plan plan_w4a16(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, i
   } else if (splits >= 2 && tiles <= kMaxCutTiles) {
     pl.ksplit = std::min(splits, pl.stages);
     if (pl.ksplit >= 2) pl.dp_tiles = 0;
-  } else if (splits == 0 && pl.stages >= 2) {
-    const int waves = (tiles + cus - 1) / cus;
-    const double eff = (double)tiles / ((double)waves * cus);
-    if (eff < 0.92) {
-      const int dp = (tiles / cus) * cus;
-      const int rem = tiles - dp;
-      double best = (double)((rem + cus - 1) / cus);
-      int best_k = 1;
-      for (int k = 2; k <= std::min(pl.stages, 16); ++k) {
-        const double t = (double)(((int64_t)rem * k + cus - 1) / cus) / k + 0.01 * k;
-        if (t < best - 1e-9) {
-          best = t;
-          best_k = k;
-        }
-      }
-      if (best_k > 1 && rem <= kMaxCutTiles) {
-        pl.dp_tiles = dp;
-        pl.ksplit = best_k;
-      }
-    }
+  } else if (splits == 0) {
+    pl.ksplit = four_wave_pieces(tiles, pl.stages, cus, &pl.dp_tiles);
   }
   pl.grid = pl.dp_tiles + (tiles - pl.dp_tiles) * pl.ksplit;
   const size_t partial_bytes = (pl.dp_tiles < tiles && !direct && (!is_tile256(pl.cfg) || pl.ksplit > 1))
