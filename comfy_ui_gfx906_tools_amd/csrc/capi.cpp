@@ -122,9 +122,11 @@ int tile256_pieces(int tiles, int stages, int splits, int cfg, int cus) {
 }
 
 // K pieces of the 4-wave kernel (configurations 0-3) with splits 0: when the last round of tiles
-// fills the CUs badly (under 92%), its tiles are cut into the k pieces that minimize the modelled
-// time ceil(rem k / CUs) / k (+ 1% per piece for the partial round trip); *dp = the tiles that
-// run whole (the full rounds), the rest are cut. Returns 1 when nothing is cut (*dp = tiles).
+// fills the CUs badly (under 92%), its tiles are cut into as many K pieces as fit one round of
+// workgroups, k = CUs / rem (at most 16 and the stage count); *dp = the tiles that run whole (the
+// full rounds), the rest are cut. Returns 1 when nothing is cut (*dp = tiles). A second round of
+// pieces costs more than its shorter pieces save (MI355X, K = 3072, N = 18432, weights from HBM,
+// 72 tiles: 3 pieces 29.4 / 40.2 us at M = 64 / 128, 7 pieces in two rounds 36.9 / 61.2 us).
 int four_wave_pieces(int tiles, int stages, int cus, int* dp) {
   *dp = tiles;
   if (stages < 2) return 1;
@@ -132,18 +134,10 @@ int four_wave_pieces(int tiles, int stages, int cus, int* dp) {
   if ((double)tiles / ((double)waves * cus) >= 0.92) return 1;
   const int whole = (tiles / cus) * cus;
   const int rem = tiles - whole;
-  double best = (double)((rem + cus - 1) / cus);
-  int best_k = 1;
-  for (int k = 2; k <= std::min(stages, 16); ++k) {
-    const double t = (double)(((int64_t)rem * k + cus - 1) / cus) / k + 0.01 * k;
-    if (t < best - 1e-9) {
-      best = t;
-      best_k = k;
-    }
-  }
-  if (best_k == 1 || rem > kMaxCutTiles) return 1;
+  const int k = std::min(std::min(cus / rem, stages), 16);
+  if (k < 2 || rem > kMaxCutTiles) return 1;
   *dp = whole;
-  return best_k;
+  return k;
 }
 
 // 256 x 256 tiles once there are at least a quarter as many as CUs. Measured on MI355X (bf16 x via
@@ -205,19 +199,25 @@ int w4a16_cfg_for(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, int 
   if (M <= 64) return 2;
   if (M <= 128) return 1;
   if (splits < 2 && prefer_tile256(M, N, K, cus)) return kCfgTile256Auto;
-  // Fewer 256 x 256 tiles than that: the 128-row tiles with K pieces, unless their pieces need
-  // more than one round of workgroups; then the 256 x 256 tiles cut into K pieces (one round)
-  // win. Measured on MI355X, fp16 x, weights from HBM, us 128-row plan vs 256 x 256 pieces: over
-  // one round M=768 K=3072 N=3072 (504 workgroups) 57.6 vs 41.7, M=1024 480 workgroups 57.2 vs
-  // 44.2, M=512 N=6144 53.8 vs 43.3, M=768 and 1024 at K=12288 89.1 vs 76.3 and 107.7 vs 90.9;
-  // one round or less M=512 N=3072 29.8 vs 35.0, K=12288 55.9 vs 57.9, M=640 30.3 vs 39.3,
-  // M=896 37.0 vs 41.6, M=1024 N=2048 31.6 vs 40.0, M=256 K=4096 N=10240 41.9 vs 45.2.
+  // Fewer 256 x 256 tiles than that: the 128-row tiles with K pieces (one round), unless that round
+  // leaves more than a tenth of the CUs idle and the 256 x 256 tiles' own K pieces (one round, at
+  // a quarter of the tiles) are at least 16 stages long; shorter pieces spend more on pipeline
+  // fill and partials than the fuller round gains. Measured on MI355X, fp16 x, weights from HBM,
+  // us 128-row round vs 256 x 256 pieces: K = 12288, N = 3072: M = 768 (84% of the CUs) 81.9 vs
+  // 78.5, M = 1024 (75%) 104.8 vs 91.7, M = 512 (94%) 55.9 vs 57.9; K = 3072 (pieces of 7-10
+  // stages): M = 768 38.3 vs 43.1, M = 1024 42.8 vs 45.4, N = 6144 M = 512 42.6 vs 44.8, and at
+  // 94-100% M = 512 / 640 / 896 and N = 2048 M = 1024 30.6 / 31.2 / 37.0 / 32.4 vs 40.6 / 43.7 /
+  // 41.6 / 46.9.
   if (splits == 0 && K % 64 == 0) {
     const W4A16Config& c = w4a16_config(1);
     const int tiles = (int)(((M + c.BM - 1) / c.BM) * ((N + c.BN - 1) / c.BN));
     int dp = tiles;
     const int k = four_wave_pieces(tiles, w4a16_steps(1, K), cus, &dp);
-    if (dp + (int64_t)(tiles - dp) * k > cus) return kCfgTile256Auto;
+    const int64_t grid = dp + (int64_t)(tiles - dp) * k;
+    const int t256 = (int)(((M + 255) / 256) * ((N + 255) / 256));
+    const int stages = (int)(K / 64);
+    const int k256 = tile256_pieces(t256, stages, 0, kCfgTile256Auto, cus);
+    if (10 * grid < 9 * (int64_t)cus && stages / k256 >= 16) return kCfgTile256Auto;
   }
   return 1;
 }

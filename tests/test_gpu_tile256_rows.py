@@ -118,23 +118,26 @@ def test_rows_k_pieces_vs_whole_tiles(M):
     assert (np.abs(cut - whole) <= bound).all()
 
 
-@pytest.mark.parametrize("M,N,K", [(768, 3072, 3072), (1024, 3072, 3072), (1000, 2600, 2048)])
-def test_auto_plan_two_round_shapes_take_256_tiles_with_k_pieces(M, N, K):
-    """Between 129 rows and a quarter of the CUs in 256 x 256 tiles, the automatic plan takes the
-    256 x 256 tiles cut into K pieces (one round of workgroups) wherever the 128-row tiles' K
-    pieces would need two rounds; against the float64 oracle (gate), fp32 and bf16 out with bias."""
+@pytest.mark.parametrize("M,N,K,cfg", [(768, 3072, 12288, 5), (1024, 3072, 12288, 5), (1000, 2600, 8192, 5),
+                                       (1024, 3072, 3072, 1), (768, 3072, 3072, 1), (128, 18432, 3072, 1),
+                                       (40, 18432, 3072, 2)])
+def test_auto_plan_one_round_of_k_pieces(M, N, K, cfg):
+    """Fewer 256 x 256 tiles than a quarter of the CUs: the automatic plan cuts K into pieces that
+    fit one round of workgroups, on the 128- or 64-row tiles, or on the 256 x 256 tiles where the
+    128-row round leaves CUs idle and the 256 x 256 pieces stay long (K = 8192, 12288); against
+    the float64 oracle (gate), fp32 and bf16 out with bias."""
     L = _lib()
     plan = L.w4a16_describe_plan(M, N, K, cus=256)
-    assert (plan["config"], plan["tile_rows"]) == (5, 256) and plan["k_pieces"] > 1
-    assert plan["tiles"] * plan["k_pieces"] <= 256
-    print(f"case auto two-round M={M} N={N} K={K} plan={plan}", flush=True)
+    assert plan["config"] == cfg and plan["k_pieces"] > 1
+    assert plan["whole_tiles"] + (plan["tiles"] - plan["whole_tiles"]) * plan["k_pieces"] <= 256
+    print(f"case auto one-round M={M} N={N} K={K} plan={plan}", flush=True)
     x, wq, ws = seeded_linear(M, N, K, seed=M + N + K)
     bias = torch.randn(N, generator=torch.Generator().manual_seed(M))
     xd, wqd, wsd = x.to(DEV), wq.to(DEV), ws.to(DEV)
-    y = _lib().w4a16_gemm(xd, wqd, wsd, bias.to(DEV), out_dtype=torch.float32)
+    y = L.w4a16_gemm(xd, wqd, wsd, bias.to(DEV), out_dtype=torch.float32)
     ref = orc.w4a16_reference(to_np_f32(x), wq.numpy(), ws.numpy(), bias.numpy())
     assert rel_max_err(to_np_f32(y), ref) <= TOL
-    yb = to_np_f32(_lib().w4a16_gemm(xd, wqd, wsd, bias.to(torch.bfloat16).to(DEV), out_dtype=torch.bfloat16))
+    yb = to_np_f32(L.w4a16_gemm(xd, wqd, wsd, bias.to(torch.bfloat16).to(DEV), out_dtype=torch.bfloat16))
     refb = orc.w4a16_reference(to_np_f32(x), wq.numpy(), ws.numpy(), to_np_f32(bias.to(torch.bfloat16))).astype(np.float32)
     ref_r = orc.round_to_dtype(refb, "bfloat16")
     assert (np.abs(yb - ref_r) <= bf16_ulp(ref_r) + TOL * np.abs(refb).max()).all()
