@@ -105,3 +105,21 @@ def test_describe_plan_row_tiles():
     assert (d["whole_tiles"], d["k_pieces"]) == (0, 3)
     d = _lib.w4a16_describe_plan(64, 10240, 4096, config=5, splits=1, cus=256)
     assert (d["whole_tiles"], d["k_pieces"]) == (40, 1)
+
+
+@pytest.mark.parametrize("cus", [80, 256, 304])
+def test_w4a16_k_pieces_fit_one_round(cus):
+    """Automatic plans (splits 0): the K pieces of the cut tiles fit one round of workgroups after
+    the whole rounds, on both tile kernels (a second round of pieces measured 20-35% slower)."""
+    from comfy_ui_gfx906_tools_amd import _lib
+    if not os.path.exists(LIB):
+        pytest.skip("libqlinear.so not built")
+    import torch
+    for M, N, K in itertools.product([17, 64, 100, 128, 200, 512, 768, 1024, 2049], [3072, 9216, 18432, 21504],
+                                     [1024, 3072, 12288]):
+        for xdt in (torch.float16, torch.bfloat16):
+            d = _lib.w4a16_describe_plan(M, N, K, x_dtype=xdt, cus=cus)
+            if d["config"] > 6 or d["k_pieces"] == 1:
+                continue
+            cut = d["tiles"] - d["whole_tiles"]
+            assert cut * d["k_pieces"] <= cus, (M, N, K, xdt, cus, d)
