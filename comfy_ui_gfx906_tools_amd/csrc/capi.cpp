@@ -121,6 +121,18 @@ int tile256_pieces(int tiles, int stages, int splits, int cfg, int cus) {
   return std::max(1, std::min(cus / tiles, stages / kMinPieceStages));
 }
 
+// 224-row tiles instead of 256 when the 256-row tiles make a single round that leaves CUs idle
+// (more than half but not all of them busy) and 224-row tiles still fit one round with more CUs
+// busy: each tile has 7/8 of the MFMA work (the same dequant). fc2 of the C2 pair (4608 x 3072):
+// 216 -> 252 tiles on 256 CUs, 294.9 -> 289.3 us; C1 81.1 -> 79.6 us; the DiT's 4096-row img
+// proj / fc2 (4096 x 3072): 192 -> 228 tiles, 0.5% faster. More CUs busy lower the power-limited
+// clock, which takes back most of the gain. Results are bit-identical to the 256-row tiles.
+bool tile224_fits(int64_t M, int64_t N, int cus) {
+  const int64_t tn = (N + 255) / 256;
+  const int64_t t256 = (M + 255) / 256 * tn, t224 = (M + 223) / 224 * tn;
+  return 2 * t256 > cus && t256 < cus && t224 <= cus && t224 > t256;
+}
+
 // K pieces of the 4-wave kernel (configurations 0-3) with splits 0: when the last round of tiles
 // fills the CUs badly (under 92%), its tiles are cut into as many K pieces as fit one round of
 // workgroups, k = CUs / rem (at most 16 and the stage count); *dp = the tiles that run whole (the
@@ -240,8 +252,10 @@ W4A16Plan plan_w4a16(int x_dtype, int64_t M, int64_t N, int64_t K, int splits, i
     pl.BN = 16 * skinny_blocks(M, N, cus);
     pl.stages = 1;
   } else if (is_tile256(pl.cfg)) {
-    // variant 1 (configuration 5) takes the shortest tile height that covers M, 64 / 128 / 256
+    // variant 1 (configuration 5) takes the shortest tile height that covers M, 64 / 128 / 256,
+    // or 224 rows where that fills more CUs in the same single round (tile224_fits)
     pl.BM = pl.cfg != kCfgTile256Auto ? 256 : M <= 64 ? 64 : M <= 128 ? 128 : 256;
+    if (pl.cfg == kCfgTile256Auto && pl.BM == 256 && splits == 0 && tile224_fits(M, N, cus)) pl.BM = 224;
     pl.BN = 256;
     pl.stages = (int)(K / 64);
   } else {
@@ -624,8 +638,11 @@ int qlinear_check_launch_plan(int op, int x_dtype, int64_t M, int64_t N, int64_t
     if (pl.dp_tiles < 0 || pl.dp_tiles > tiles) return fail(QL_ERR_SHAPE, "dp_tiles %d of %d", pl.dp_tiles, tiles);
     if (is_tile256(pl.cfg) && (pl.BM != 256 || pl.ksplit > 1)) {
       // variant 1 with BM-row tiles: all whole, or all cut into ksplit K pieces (partials + reduce)
-      if (pl.cfg != kCfgTile256Auto || (pl.BM != 64 && pl.BM != 128 && pl.BM != 256))
+      if (pl.cfg != kCfgTile256Auto || (pl.BM != 64 && pl.BM != 128 && pl.BM != 224 && pl.BM != 256))
         return fail(QL_ERR_SHAPE, "tile256 rows: configuration %d with %d-row tiles", pl.cfg, pl.BM);
+      if (pl.BM == 224 && (pl.ksplit != 1 || pl.dp_tiles != tiles || tiles > cus))
+        return fail(QL_ERR_SHAPE, "tile256 rows: 224-row tiles are one round of whole tiles (%d of %d, ksplit %d)",
+                    pl.dp_tiles, tiles, pl.ksplit);
       if (pl.ksplit > 1 && pl.dp_tiles != 0)
         return fail(QL_ERR_SHAPE, "tile256 rows: %d whole tiles beside K pieces", pl.dp_tiles);
       if (pl.ksplit < 1 || pl.ksplit > pl.stages)

@@ -81,15 +81,18 @@ template <bool kBf16, int kWavesM, int kWavesN, int WM, int WN, int kSub, bool k
 __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W4A16Params p) {
   constexpr int kWaves = kWavesM * kWavesN;
   constexpr int BM = 32 * WM * kWavesM, BN = 32 * WN * kWavesN;
-  constexpr int kABytes = BM * kT256StageK * 2;  // activations: BM rows x 128 B
+  // activation rows of a stage buffer: BM rounded up to whole DMA rounds (8 rows per wave); the
+  // rows past BM (224-row tiles: 224 .. 255) lie outside the activation descriptor and read zeros
+  constexpr int kARows = (BM + 8 * kWavesM * kWavesN - 1) / (8 * kWavesM * kWavesN) * (8 * kWavesM * kWavesN);
+  constexpr int kABytes = kARows * kT256StageK * 2;  // activations: kARows rows x 128 B
   constexpr int kBBytes = BN * kT256StageK / 2;  // weights: BN columns x 32 B
   constexpr int kSBytes = BN * 2 * 4;            // scales: BN columns x 2 groups x 4 B
   constexpr int kStageBytes = kABytes + kBBytes + kSBytes;
   // DMA instructions per wave and stage: activations in 1 KiB blocks (8 rows), weights in 1 KiB
   // blocks (32 columns), scales in 256 B blocks (32 columns)
-  constexpr int nA = BM / 8 / kWaves, nB = BN / 32 / kWaves, nS = BN / 32 / kWaves;
+  constexpr int nA = kARows / 8 / kWaves, nB = BN / 32 / kWaves, nS = BN / 32 / kWaves;
   constexpr int nL = nA + nB + nS;
-  static_assert(nA * 8 * kWaves == BM && nB * 32 * kWaves == BN && nB >= 1, "DMA blocks must split evenly");
+  static_assert(nA * 8 * kWaves == kARows && nB * 32 * kWaves == BN && nB >= 1, "DMA blocks must split evenly");
   static_assert(nL <= 4 * WM * WN, "the loads of a stage are spread over the MFMAs of a stage");
   static_assert(kNBuf >= 3 && kNBuf * kStageBytes <= 160 * 1024, "stage ring: 3 or more buffers in 160 KiB of LDS");
   __shared__ __attribute__((aligned(1024))) uint8_t lds[kNBuf * kStageBytes];
@@ -488,13 +491,14 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W
           }
       }
     } else {
-      // 16-bit outputs go through LDS, half a tile (BM/2 rows x BN columns) at a time, so that
+      // 16-bit outputs go through LDS, half a tile (kHalfRows rows x BN columns) at a time, so that
       // each wave stores whole 512-byte row segments with 16-byte lanes instead of 8-byte pieces
       // of 32 different rows. LDS row r holds 16-byte chunk c at slot c ^ (r & 31): the 8-byte
       // writes of a wave (32 rows x 2 halves of one chunk) and the 16-byte reads (2 rows x 32
       // chunks) are both conflict free. The stage buffers are free once every wave is past its
       // last MFMA and the DMA loads issued for stages past the end (which write zeros) have landed.
-      constexpr int kHalfRows = BM / 2;
+      // halves of whole 32-row blocks: BM / 2, or 128 + 96 rows for 224-row tiles
+      constexpr int kHalfRows = (BM / 2 + 31) / 32 * 32;
       constexpr int kChunks = BN / 8;  // 16-byte chunks per row
       static_assert(kHalfRows * BN * 2 <= kNBuf * kStageBytes, "half a tile must fit the stage buffers");
       wait_vmcnt<0>();
@@ -532,7 +536,8 @@ __global__ __launch_bounds__(64 * kWavesM * kWavesN) void w4a16_tile256_kernel(W
           const int r = q / kChunks, c = q % kChunks;
           u32x4 v = *(const u32x4*)(lds + r * (BN * 2) + ((c ^ (r & 31)) << 4));
           const int m = m0 + half * kHalfRows + r, n = n0 + 8 * c;
-          if (m < M && n < N) {
+          // (a short second half, 224-row tiles: staged rows past the tile are not this tile's)
+          if (half * kHalfRows + r < BM && m < M && n < N) {
             uint16_t* dst = (uint16_t*)p.y + (size_t)m * N + n;
             if constexpr ((kOdt == kBF16 || kOdt == kF16) && kResidual) {
               if (p.residual)  // gated residual on the rounded outputs (uniform over the workgroup)
@@ -621,17 +626,29 @@ hipError_t launch_rows(const W4A16Params& p, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// Variant 1 with 224-row tiles, all whole: a single round of tiles where 256-row tiles would leave
+// CUs idle (the plan takes it only then; the activation stages keep the 256-row layout).
+template <bool kBf16>
+hipError_t launch_rows224(const W4A16Params& p, hipStream_t stream) {
+  if (p.ksplit != 1 || p.dp_tiles != p.tiles_m * p.tiles_n) return hipErrorInvalidValue;
+  W4A16Params q = p;
+  q.tile_base = 0;
+  hipLaunchKernelGGL((w4a16_tile256_kernel<kBf16, 1, 8, 7, 1, 1>), dim3(p.dp_tiles), dim3(512), 0, stream, q);
+  return hipGetLastError();
+}
+
 }  // namespace
 
 hipError_t w4a16_tile256_launch(int variant, bool bf16, const W4A16Params& p, hipStream_t stream) {
   switch (variant) {
     case 0:  // 8 waves, 2 x 4, each 128 x 64
       return bf16 ? launch_variant<true, 2, 4, 4, 2>(p, stream) : launch_variant<false, 2, 4, 4, 2>(p, stream);
-    case 1:  // 8 waves, 1 x 8, each 256 x 32; with K pieces, or 64 / 128-row tiles, per the plan
+    case 1:  // 8 waves, 1 x 8, each 256 x 32; with K pieces, or 64 / 128 / 224-row tiles, per the plan
       if (p.ksplit > 1 || p.tile_rows != 256) {
         switch (p.tile_rows) {
           case 64: return bf16 ? launch_rows<true, 2>(p, stream) : launch_rows<false, 2>(p, stream);
           case 128: return bf16 ? launch_rows<true, 4>(p, stream) : launch_rows<false, 4>(p, stream);
+          case 224: return bf16 ? launch_rows224<true>(p, stream) : launch_rows224<false>(p, stream);
           case 256: return bf16 ? launch_rows<true, 8>(p, stream) : launch_rows<false, 8>(p, stream);
           default: return hipErrorInvalidValue;
         }

@@ -76,7 +76,9 @@ def test_describe_plan():
     fc1 = _lib.w4a16_describe_plan(4608, 12288, 3072, cus=256)
     assert (fc1["config"], fc1["tile_rows"], fc1["tiles"], fc1["whole_tiles"], fc1["staged"]) == (5, 256, 864, 768, True)
     fc2 = _lib.w4a16_describe_plan(4608, 3072, 12288, cus=256, x_dtype=__import__("torch").float16)
-    assert (fc2["config"], fc2["tiles"], fc2["whole_tiles"], fc2["staged"]) == (5, 216, 216, False)
+    # 216 tiles of 256 rows would leave 40 CUs idle: 252 tiles of 224 rows, one round
+    assert (fc2["config"], fc2["tile_rows"], fc2["tiles"], fc2["whole_tiles"], fc2["staged"]) == (5, 224, 252, 252, False)
+    assert _lib.w4a16_describe_plan(4608, 3072, 12288, cus=256, splits=1)["tile_rows"] == 256
     assert _lib.w4a16_describe_plan(1, 10240, 4096, cus=256)["config"] == 7
     assert _lib.w4a16_describe_plan(16, 10240, 4096, cus=256)["config"] == 8
     assert _lib.w4a16_describe_plan(64, 10240, 4096, cus=256)["config"] == 2
