@@ -121,8 +121,8 @@ def cpu_baseline(x_bf16, w1, s1, b1, w2, s2, b2, repeats):
 def main():
     args = parse()
     if args.gpus != 1:
-        print(json.dumps({"error": "this build runs on one GPU: the W4A16 path is measured on a single MI355X; "
-                                   "multi-GPU sharding is described in DESIGN.md and not launched",
+        print(json.dumps({"error": "this build runs on one GPU: the W4A16 path is measured on a single MI355X "
+                                   "and no multi-GPU sharding is launched",
                           "n_gpus": args.gpus}))
         sys.exit(2)
     if args.calibrate_copy:
