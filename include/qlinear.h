@@ -112,10 +112,10 @@ typedef struct ql_w4a16_residual {
 } ql_w4a16_residual;
 /* flags bits 8-11: 0 = automatic kernel choice, c + 1 = force kernel configuration c
  * (0-3: 256 / 128 / 64 / 16-row x 256-column tiles, 4 waves; 4-6: 256-column tiles with 8 waves
- * as 2 x 4, 8 waves as 1 x 8, 4 waves as 1 x 4, K % 64 == 0; 4 and 6 256 x 256 whole tiles,
- * 5 (1 x 8) with the tile height and K pieces its plan picks: 64 / 128 rows for M <= 64 / 128,
- * else 256 (224 where that fills a single round better), K pieces when the tiles fill at most a
- * third of the CUs, 128-row halves for a last round at most half full; 7: M <= 4,
+ * as 2 x 4, 8 waves as 1 x 8, 4 waves as 1 x 4, K % 64 == 0; 256 x 256 tiles, a last round at
+ * most half full run as 128-row halves; 5 also takes the tile height and K pieces its plan
+ * picks: 64 / 128 rows for M <= 64 / 128, 224 rows where that fills a single round better, and
+ * K pieces (fp32 partials summed in order) when the tiles fill at most a third of the CUs; 7: M <= 4,
  * K <= 8192, bfloat16/float16 x read as given, VALU dot products on the exact integer codes with
  * the group scale applied in fp32 -- the automatic choice for M = 1; 8: M <= 16, K % 128 == 0,
  * K <= 4096, bfloat16/float16 x read as given, MFMA on the exact integer codes with the group
