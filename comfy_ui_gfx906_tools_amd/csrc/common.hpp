@@ -141,6 +141,31 @@ __device__ __forceinline__ float gelu_tanh(float x) {
   return x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(t));
 }
 
+// rint(fl(v / s)) of a quantizer whose codes satisfy |v / s| <= 128 (scale s = amax * c,
+// c <= 1/7), bit for bit, with a multiplication by r = fl(1 / s) (computed once per scale) in
+// place of the division: v r = (v / s)(1 + d1)(1 + d2) with |d1|, |d2| <= 2^-24 lies within
+// 128 * 2^-23 (1 + 2^-24) < 2^-15.9 of v / s, so the two round to the same integer unless v / s
+// lies that close to a half-integer (ties go to even in both). Those, and NaN, take the exact
+// quotient: where |frac(v r) - 1/2| <= 2^-15. (y - floor(y) is exact for |y| < 2^23.)
+__device__ __forceinline__ bool quot_near_half(float y) { return !(fabsf((y - floorf(y)) - 0.5f) > 0x1p-15f); }
+// N values at a time: the multiplications for all of them, the exact quotients only in a block
+// that a wave skips unless one of its lanes needs it (one value in about 2^13)
+template <int N>
+__device__ __forceinline__ void rint_quot_n(const float* v, float s, float r, float* q) {
+  bool need = false;
+#pragma unroll
+  for (int e = 0; e < N; ++e) {
+    const float y = __fmul_rn(v[e], r);
+    q[e] = rintf(y);
+    need |= quot_near_half(y);
+  }
+  if (need) {
+#pragma unroll
+    for (int e = 0; e < N; ++e)
+      if (quot_near_half(__fmul_rn(v[e], r))) q[e] = rintf(__fdiv_rn(v[e], s));
+  }
+}
+
 // ---- compile-time loops ----------------------------------------------------------------------
 // static_for<B, E>(f) calls f(std::integral_constant<int, i>{}) for i = B .. E-1 as straight-line
 // code: the index is a constant expression inside f, so register arrays indexed by it stay in

@@ -154,14 +154,17 @@ __global__ __launch_bounds__(256) void adaln_to_f16_kernel(const void* __restric
   if constexpr (OUT == kOperandI8) {
     const float s = __fmul_rn(fmaxf(amax, 1e-8f), 1.0f / 127.0f);
     if (threadIdx.x == 0) row_scale[blockIdx.x] = s;
+    const float rcp = __fdiv_rn(1.0f, s);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int k = threadIdx.x * 8 + r * 2048;
       if (k < K) {
         uint32_t w[2] = {0u, 0u};
+        float qv[8];
+        rint_quot_n<8>(v[r], s, rcp, qv);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const int c = (int)fminf(fmaxf(rintf(__fdiv_rn(v[r][e], s)), -127.0f), 127.0f);
+          const int c = (int)fminf(fmaxf(qv[e], -127.0f), 127.0f);
           w[e >> 2] |= ((uint32_t)c & 0xFFu) << (8 * (e & 3));
         }
         typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -280,14 +283,17 @@ __global__ __launch_bounds__(256) void heads_to_f16_kernel(const void* __restric
   if constexpr (OUT == kOperandI8) {  // the rule of qlinear_quantize_int8_per_token
     const float s = __fmul_rn(fmaxf(amax, 1e-8f), 1.0f / 127.0f);
     if (threadIdx.x == 0) row_scale[l] = s;
+    const float rcp = __fdiv_rn(1.0f, s);
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const int p = threadIdx.x * 8 + r * 2048;
       if (p < Kt) {
         uint32_t w[2] = {0u, 0u};
+        float qv[8];
+        rint_quot_n<8>(v[r], s, rcp, qv);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          const int c = (int)fminf(fmaxf(rintf(__fdiv_rn(v[r][e], s)), -127.0f), 127.0f);
+          const int c = (int)fminf(fmaxf(qv[e], -127.0f), 127.0f);
           w[e >> 2] |= ((uint32_t)c & 0xFFu) << (8 * (e & 3));
         }
         typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));

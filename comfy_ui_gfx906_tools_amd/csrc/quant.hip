@@ -61,10 +61,13 @@ __global__ __launch_bounds__(kQThreads) void quantize_int4_kernel(const void* __
   for (int e = 0; e < 32; ++e) amax = fmaxf(amax, fabsf(v[e]));
   amax = fmaxf(amax, 1e-8f);
   const float s = rule == 0 ? __fdiv_rn(amax, 7.0f) : __fmul_rn(amax, 1.0f / 7.0f);
+  const float rcp = __fdiv_rn(1.0f, s);
   u32x4 out = {0u, 0u, 0u, 0u};
+  float qv[32];
+  rint_quot_n<32>(v, s, rcp, qv);
 #pragma unroll
   for (int e = 0; e < 32; ++e) {
-    const float q = fminf(fmaxf(rintf(__fdiv_rn(v[e], s)), -8.0f), 7.0f);
+    const float q = fminf(fmaxf(qv[e], -8.0f), 7.0f);
     out[e / 8] |= ((uint32_t)(int)q & 0xFu) << (4 * (e % 8));
   }
   packed[b] = out;
@@ -90,9 +93,12 @@ __global__ __launch_bounds__(kQThreads) void quantize_int8_row_kernel(const void
   for (int w = 1; w < kQThreads / kWave; ++w) amax = fmaxf(amax, red[w]);
   const float s = __fmul_rn(fmaxf(amax, 1e-8f), 1.0f / 127.0f);
   if (threadIdx.x == 0) scale[row] = s;
+  const float rcp = __fdiv_rn(1.0f, s);
   for (int k = threadIdx.x; k < K; k += kQThreads) {
     const float v = read_elem(x, DT, base + k);
-    q[base + k] = (int8_t)(int)fminf(fmaxf(rintf(__fdiv_rn(v, s)), -127.0f), 127.0f);
+    float qv;
+    rint_quot_n<1>(&v, s, rcp, &qv);
+    q[base + k] = (int8_t)(int)fminf(fmaxf(qv, -127.0f), 127.0f);
   }
 }
 
@@ -147,14 +153,17 @@ __global__ __launch_bounds__(kQThreads) void quantize_int8_row_vec_kernel(const 
   for (int w = 1; w < kQThreads / kWave; ++w) amax = fmaxf(amax, red[w]);
   const float s = __fmul_rn(fmaxf(amax, 1e-8f), 1.0f / 127.0f);
   if (threadIdx.x == 0) scale[row] = s;
+  const float rcp = __fdiv_rn(1.0f, s);
 #pragma unroll
   for (int i = 0; i < kQ8Vec; ++i) {
     const int vi = threadIdx.x + i * kQThreads;
     if (vi < nv) {
       uint32_t lo = 0, hi = 0;
+      float qv[8];
+      rint_quot_n<8>(v[i], s, rcp, qv);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const uint32_t c = (uint32_t)(int)fminf(fmaxf(rintf(__fdiv_rn(v[i][e], s)), -127.0f), 127.0f) & 0xFFu;
+        const uint32_t c = (uint32_t)(int)fminf(fmaxf(qv[e], -127.0f), 127.0f) & 0xFFu;
         if (e < 4)
           lo |= c << (8 * e);
         else
@@ -231,13 +240,16 @@ __global__ __launch_bounds__(kQThreads) void quantize_int8_block32_kernel(const 
 #pragma unroll
   for (int e = 0; e < 32; ++e) amax = fmaxf(amax, fabsf(v[e]));
   const float s = __fmul_rn(fmaxf(amax, 1e-8f), 1.0f / 127.0f);
+  const float rcp = __fdiv_rn(1.0f, s);
   u32x4 out[2];
+  float qv[32];
+  rint_quot_n<32>(v, s, rcp, qv);
 #pragma unroll
   for (int w = 0; w < 8; ++w) {
     uint32_t word = 0;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const int c = (int)fminf(fmaxf(rintf(__fdiv_rn(v[4 * w + e], s)), -127.0f), 127.0f);
+      const int c = (int)fminf(fmaxf(qv[4 * w + e], -127.0f), 127.0f);
       word |= (uint32_t)(c & 0xFF) << (8 * e);
     }
     out[w >> 2][w & 3] = word;
